@@ -1,0 +1,289 @@
+// C entry points of kernels.so: argument validation, error state, device
+// queries, workspace and launch planning.  The kernels live in the other
+// translation units; every launcher here is host code only.
+#include <stdarg.h>
+#include <stdio.h>
+#include <string.h>
+
+#include <mutex>
+
+#include "xattn_common.h"
+#include "xattn_launch.h"
+
+namespace xattn {
+
+// --------------------------------------------------------------------------
+// Error state (per host thread, first error wins until read)
+// --------------------------------------------------------------------------
+static thread_local int g_err = XATTN_OK;
+static thread_local char g_msg[512] = "";
+
+void set_error(int code, const char* fmt, ...) {
+    char buf[512];
+    va_list ap;
+    va_start(ap, fmt);
+    vsnprintf(buf, sizeof(buf), fmt, ap);
+    va_end(ap);
+    if (g_err == XATTN_OK) g_err = code;
+    snprintf(g_msg, sizeof(g_msg), "%s", buf);
+}
+
+bool check_launch(const char* who) {
+    const hipError_t e = hipPeekAtLastError();
+    if (e != hipSuccess) {
+        set_error(XATTN_ERR_LAUNCH, "%s: launch failed: %s", who, hipGetErrorString(e));
+        return false;
+    }
+    return true;
+}
+
+// --------------------------------------------------------------------------
+// Device properties (cached per device)
+// --------------------------------------------------------------------------
+static std::mutex g_dev_mu;
+static int g_cu[256];
+static int g_lds[256];
+
+int device_max_lds() {
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 256) return 64 * 1024;
+    std::lock_guard<std::mutex> lk(g_dev_mu);
+    if (g_lds[dev] <= 0) {
+        int lds = 0;
+        if (hipDeviceGetAttribute(&lds, hipDeviceAttributeMaxSharedMemoryPerBlock, dev) !=
+                hipSuccess ||
+            lds <= 0)
+            lds = 64 * 1024;
+        g_lds[dev] = lds;
+    }
+    return g_lds[dev];
+}
+
+int device_cu_count() {
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 256) return 256;
+    std::lock_guard<std::mutex> lk(g_dev_mu);
+    if (g_cu[dev] <= 0) {
+        int cu = 0;
+        if (hipDeviceGetAttribute(&cu, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
+            cu <= 0)
+            cu = 256;
+        g_cu[dev] = cu;
+    }
+    return g_cu[dev];
+}
+
+// --------------------------------------------------------------------------
+// Library-owned split workspace for launch_optimized_kernel (grow-only).
+// --------------------------------------------------------------------------
+static std::mutex g_ws_mu;
+static void* g_ws_ptr[256];
+static size_t g_ws_bytes[256];
+
+static void* workspace(size_t bytes) {
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 256) {
+        set_error(XATTN_ERR_ALLOC, "workspace: no current device");
+        return nullptr;
+    }
+    std::lock_guard<std::mutex> lk(g_ws_mu);
+    if (g_ws_bytes[dev] < bytes) {
+        if (g_ws_ptr[dev]) {
+            // Earlier launches may still read the old block.
+            (void)hipDeviceSynchronize();
+            (void)hipFree(g_ws_ptr[dev]);
+            g_ws_ptr[dev] = nullptr;
+            g_ws_bytes[dev] = 0;
+        }
+        void* p = nullptr;
+        if (hipMalloc(&p, bytes) != hipSuccess) {
+            (void)hipGetLastError();
+            set_error(XATTN_ERR_ALLOC, "workspace: hipMalloc(%zu) failed", bytes);
+            return nullptr;
+        }
+        g_ws_ptr[dev] = p;
+        g_ws_bytes[dev] = bytes;
+    }
+    return g_ws_ptr[dev];
+}
+
+// --------------------------------------------------------------------------
+// Validation
+// --------------------------------------------------------------------------
+bool validate_common(const char* who, const void* Q, const void* K, const void* V,
+                     const void* out, int B, int NL, int NI, int dim) {
+    if (B < 0 || NL < 0 || NI < 0 || dim < 0) {
+        set_error(XATTN_ERR_INVALID_VALUE, "%s: negative size (B=%d NL=%d NI=%d dim=%d)", who, B,
+                  NL, NI, dim);
+        return false;
+    }
+    if ((long long)B * NL > 0 && (!Q || !out)) {
+        set_error(XATTN_ERR_INVALID_VALUE, "%s: NULL Q/output", who);
+        return false;
+    }
+    if ((long long)B * NI > 0 && (!K || !V)) {
+        set_error(XATTN_ERR_INVALID_VALUE, "%s: NULL K/V", who);
+        return false;
+    }
+    return true;
+}
+
+bool validate_dim768(const char* who, int dim) {
+    if (dim != kDim) {
+        set_error(XATTN_ERR_UNSUPPORTED, "%s: dim=%d unsupported (built for dim=%d)", who, dim,
+                  kDim);
+        return false;
+    }
+    return true;
+}
+
+bool validate_splits(const char* who, const void* po, const void* pm, const void* pl, int B,
+                     int NL, int S) {
+    if (S < 1) {
+        set_error(XATTN_ERR_INVALID_VALUE, "%s: num_splits=%d must be >= 1", who, S);
+        return false;
+    }
+    if ((long long)B * NL > 0 && (!po || !pm || !pl)) {
+        set_error(XATTN_ERR_INVALID_VALUE, "%s: NULL split scratch", who);
+        return false;
+    }
+    return true;
+}
+
+int optimized_num_splits(int B, int NL, int NI, int cu) {
+    if (B <= 0 || NL <= 0 || NI <= 0) return 1;
+    const long long items = (long long)B * f32_row_blocks(NL);
+    if (items >= cu) return 1;
+    const int tiles = (NI + 15) / 16;
+    long long s = (cu + items - 1) / items;
+    if (s > tiles) s = tiles;
+    if (s < 1) s = 1;
+    // tile-aligned chunks: recompute the count that chunk implies
+    const int chunk_tiles = (int)((tiles + s - 1) / s);
+    return (tiles + chunk_tiles - 1) / chunk_tiles;
+}
+
+}  // namespace xattn
+
+using namespace xattn;
+
+extern "C" {
+
+int xattn_get_last_error(void) {
+    const int e = g_err;
+    g_err = XATTN_OK;
+    return e;
+}
+
+const char* xattn_get_last_error_string(void) { return g_msg; }
+
+int xattn_device_info(int device, int* cu_count, int* lds_bytes_per_block) {
+    int cu = 0, lds = 0;
+    hipError_t e = hipDeviceGetAttribute(&cu, hipDeviceAttributeMultiprocessorCount, device);
+    if (e != hipSuccess) return (int)e;
+    e = hipDeviceGetAttribute(&lds, hipDeviceAttributeMaxSharedMemoryPerBlock, device);
+    if (e != hipSuccess) return (int)e;
+    if (cu_count) *cu_count = cu;
+    if (lds_bytes_per_block) *lds_bytes_per_block = lds;
+    return 0;
+}
+
+int xattn_xcd_remap(int block, int num_blocks) { return xcd_remap(block, num_blocks); }
+
+int xattn_optimized_num_splits(int batch_size, int N_latent, int N_input, int cu_count) {
+    return optimized_num_splits(batch_size, N_latent, N_input, cu_count);
+}
+
+void launch_naive_kernel(const float* Q, const float* K, const float* V, float* output,
+                         int batch_size, int N_latent, int N_input, int dim, hipStream_t stream) {
+    const char* who = "launch_naive_kernel";
+    if (!validate_common(who, Q, K, V, output, batch_size, N_latent, N_input, dim)) return;
+    if (dim < 1) {
+        set_error(XATTN_ERR_UNSUPPORTED, "%s: dim=%d must be >= 1", who, dim);
+        return;
+    }
+    launch_naive(Q, K, V, output, batch_size, N_latent, N_input, dim, stream);
+}
+
+static bool validate_rung_dim(const char* who, int dim) {
+    if (dim < 1 || dim > kDim) {
+        set_error(XATTN_ERR_UNSUPPORTED, "%s: dim=%d outside [1, %d]", who, dim, kDim);
+        return false;
+    }
+    return true;
+}
+
+void launch_parallel_kernel(const float* Q, const float* K, const float* V, float* output,
+                            int batch_size, int N_latent, int N_input, int dim,
+                            hipStream_t stream) {
+    const char* who = "launch_parallel_kernel";
+    if (!validate_common(who, Q, K, V, output, batch_size, N_latent, N_input, dim)) return;
+    if (!validate_rung_dim(who, dim)) return;
+    const long long lds = (4LL * N_input + 4) * 4;
+    if (lds > device_max_lds()) {
+        set_error(XATTN_ERR_UNSUPPORTED,
+                  "%s: score row needs %lld B of LDS for N_input=%d, device allows %d", who, lds,
+                  N_input, device_max_lds());
+        return;
+    }
+    launch_warp(Q, K, V, output, batch_size, N_latent, N_input, dim, stream);
+}
+
+void launch_tiled_kernel(const float* Q, const float* K, const float* V, float* output,
+                         int batch_size, int N_latent, int N_input, int dim, hipStream_t stream) {
+    const char* who = "launch_tiled_kernel";
+    if (!validate_common(who, Q, K, V, output, batch_size, N_latent, N_input, dim)) return;
+    if (!validate_rung_dim(who, dim)) return;
+    launch_tiled(Q, K, V, output, batch_size, N_latent, N_input, dim, stream);
+}
+
+void launch_optimized_kernel(const float* Q, const float* K, const float* V, float* output,
+                             int batch_size, int N_latent, int N_input, int dim,
+                             hipStream_t stream) {
+    const char* who = "launch_optimized_kernel";
+    if (!validate_common(who, Q, K, V, output, batch_size, N_latent, N_input, dim)) return;
+    if (!validate_dim768(who, dim)) return;
+    if (batch_size == 0 || N_latent == 0) return;
+    const int S = optimized_num_splits(batch_size, N_latent, N_input, device_cu_count());
+    if (S <= 1) {
+        launch_flash_f32(Q, K, V, output, nullptr, nullptr, nullptr, batch_size, N_latent,
+                         N_input, 1, N_input, stream);
+        return;
+    }
+    const int tiles = (N_input + 15) / 16;
+    const int chunk = ((tiles + S - 1) / S) * 16;
+    const size_t rows = (size_t)batch_size * N_latent;
+    const size_t po_bytes = rows * S * kDim * sizeof(float);
+    const size_t ml_bytes = rows * S * sizeof(float);
+    char* ws = (char*)workspace(po_bytes + 2 * ml_bytes + 256);
+    if (!ws) return;
+    float* po = (float*)ws;
+    float* pm = (float*)(ws + po_bytes);
+    float* pl = (float*)(ws + po_bytes + ml_bytes);
+    if (!launch_flash_f32(Q, K, V, nullptr, po, pm, pl, batch_size, N_latent, N_input, S, chunk,
+                          stream))
+        return;
+    launch_lse_combine(po, pm, pl, output, (int)rows, S, stream);
+}
+
+void launch_splitk_kernel(const float* Q, const float* K, const float* V, float* output,
+                          float* po, float* pm, float* pl, int batch_size, int N_latent,
+                          int N_input, int dim, int num_splits, hipStream_t stream) {
+    const char* who = "launch_splitk_kernel";
+    if (!validate_common(who, Q, K, V, output, batch_size, N_latent, N_input, dim)) return;
+    if (!validate_dim768(who, dim)) return;
+    if (!validate_splits(who, po, pm, pl, batch_size, N_latent, num_splits)) return;
+    if (batch_size == 0 || N_latent == 0) return;
+    if ((long long)batch_size * N_latent * num_splits > 0x7fffffffLL) {
+        set_error(XATTN_ERR_INVALID_VALUE, "%s: B*NL*num_splits too large", who);
+        return;
+    }
+    // kernel_splitk.cu:59: chunk = ceil(NI / S)
+    const int chunk = (int)(((long long)N_input + num_splits - 1) / num_splits);
+    if (!launch_flash_f32(Q, K, V, nullptr, po, pm, pl, batch_size, N_latent, N_input,
+                          num_splits, chunk, stream))
+        return;
+    launch_lse_combine(po, pm, pl, output, batch_size * N_latent, num_splits, stream);
+}
+
+}  // extern "C"

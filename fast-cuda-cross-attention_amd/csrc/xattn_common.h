@@ -1,0 +1,114 @@
+// Shared device/host helpers for the gfx950 cross-attention kernels.
+//
+// Everything here is CDNA4-specific: 64-lane wavefronts, MFMA builtins,
+// LDS DMA (global_load_lds) and the 8-XCD dispatch order of MI355X.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <float.h>
+#include <stdint.h>
+
+#include "xattn.h"
+
+namespace xattn {
+
+constexpr int kWave = 64;
+constexpr int kDim = 768;              // model dimension every MFMA path is built for
+constexpr int kNumXcd = 8;             // MI355X: 8 XCDs, workgroups dealt round-robin
+
+typedef float f4 __attribute__((ext_vector_type(4)));
+typedef float f2 __attribute__((ext_vector_type(2)));
+typedef _Float16 h8 __attribute__((ext_vector_type(8)));
+typedef __bf16 bf8 __attribute__((ext_vector_type(8)));
+typedef short s8 __attribute__((ext_vector_type(8)));
+typedef unsigned short u16;
+
+// log2(e) / sqrt(768): turns a raw q.k dot product into a base-2 exponent.
+constexpr float kLog2e = 1.4426950408889634f;
+
+// --------------------------------------------------------------------------
+// Workgroup -> work-item mapping that keeps co-operating workgroups on one
+// XCD.  The dispatcher deals block b to XCD (b % 8); this returns a logical
+// index such that logical ids [off(x), off(x) + count(x)) all live on XCD x.
+// It is a bijection on [0, n) for every n (tested on the host).
+// --------------------------------------------------------------------------
+__host__ __device__ inline int xcd_remap(int bid, int n) {
+    int per = n / kNumXcd, rem = n % kNumXcd;
+    int x = bid % kNumXcd, local = bid / kNumXcd;
+    return x * per + (x < rem ? x : rem) + local;
+}
+
+// --------------------------------------------------------------------------
+// Wave-level helpers
+// --------------------------------------------------------------------------
+__device__ inline float wave_max16_groups(float v) {
+    // max over the 4 lanes {l, l^16, l^32, l^48}
+    v = fmaxf(v, __shfl_xor(v, 16));
+    v = fmaxf(v, __shfl_xor(v, 32));
+    return v;
+}
+
+__device__ inline float wave_sum16_groups(float v) {
+    v += __shfl_xor(v, 16);
+    v += __shfl_xor(v, 32);
+    return v;
+}
+
+__device__ inline float wave_sum(float v) {
+    for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o);
+    return v;
+}
+
+__device__ inline float wave_max(float v) {
+    for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o));
+    return v;
+}
+
+__device__ inline float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
+
+// s_waitcnt with only a vmcnt limit (expcnt / lgkmcnt left unconstrained).
+// gfx9 encoding: vmcnt[3:0] | expcnt[6:4] | lgkmcnt[11:8] | vmcnt_hi[15:14].
+// The waits and barriers below are also compiler fences: no memory access
+// (LDS read, DMA issue) may be moved across them, at IR level (asm memory
+// clobber) or by the machine scheduler (sched_barrier).
+__device__ inline void compiler_fence() {
+    __builtin_amdgcn_sched_barrier(0);
+    asm volatile("" ::: "memory");
+}
+
+template <int N>
+__device__ inline void wait_vmcnt() {
+    static_assert(N >= 0 && N < 64, "vmcnt range");
+    compiler_fence();
+    __builtin_amdgcn_s_waitcnt((N & 15) | (7 << 4) | (15 << 8) | ((N >> 4) << 14));
+    compiler_fence();
+}
+
+// Workgroup barrier for LDS hand-off: waits for this wave's own LDS
+// operations, then s_barrier.  Unlike __syncthreads() it carries no release
+// fence, so global->LDS DMA issued for later phases stays in flight; the
+// caller makes the DMA of the phase being consumed visible with wait_vmcnt
+// before calling this.
+__device__ inline void lds_barrier() {
+    compiler_fence();
+    __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0), vmcnt/expcnt unconstrained
+    __builtin_amdgcn_s_barrier();
+    compiler_fence();
+}
+
+// 16-byte global -> LDS DMA for one lane.  The 64 lanes of the wave land at
+// lds_base + 16 * lane (lds_base must be wave-uniform).
+__device__ inline void dma16(const void* gptr, void* lds_base) {
+    __builtin_amdgcn_global_load_lds(
+        gptr, (__attribute__((address_space(3))) void*)lds_base, 16, 0, 0);
+}
+
+}  // namespace xattn
+
+// --------------------------------------------------------------------------
+// Host-side error reporting shared by every launcher (xattn_abi.hip).
+// --------------------------------------------------------------------------
+namespace xattn {
+void set_error(int code, const char* fmt, ...);
+bool check_launch(const char* who);
+}  // namespace xattn

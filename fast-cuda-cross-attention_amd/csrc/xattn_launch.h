@@ -1,0 +1,35 @@
+// Internal (non-exported) launch helpers shared between translation units.
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+namespace xattn {
+
+int device_cu_count();
+int device_max_lds();
+int optimized_num_splits(int B, int NL, int NI, int cu);
+bool validate_common(const char* who, const void* Q, const void* K, const void* V,
+                     const void* out, int B, int NL, int NI, int dim);
+bool validate_dim768(const char* who, int dim);
+bool validate_splits(const char* who, const void* po, const void* pm, const void* pl, int B,
+                     int NL, int S);
+
+// fp32 MFMA flash kernel.  po == nullptr: normalised output over all keys
+// (S must be 1).  Otherwise: unnormalised split partials, split s covering
+// keys [s*chunk, min((s+1)*chunk, NI)).
+int f32_row_blocks(int NL);
+bool launch_flash_f32(const float* Q, const float* K, const float* V, float* out, float* po,
+                      float* pm, float* pl, int B, int NL, int NI, int S, int chunk,
+                      hipStream_t stream);
+bool launch_lse_combine(const float* po, const float* pm, const float* pl, float* out, int rows,
+                        int S, hipStream_t stream);
+
+// fp32 ladder rungs
+bool launch_naive(const float* Q, const float* K, const float* V, float* out, int B, int NL,
+                  int NI, int dim, hipStream_t stream);
+bool launch_warp(const float* Q, const float* K, const float* V, float* out, int B, int NL,
+                 int NI, int dim, hipStream_t stream);
+bool launch_tiled(const float* Q, const float* K, const float* V, float* out, int B, int NL,
+                  int NI, int dim, hipStream_t stream);
+
+}  // namespace xattn

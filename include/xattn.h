@@ -1,0 +1,141 @@
+/*
+ * xattn.h -- C ABI of kernels.so, the MI355X (gfx950) fused cross-attention
+ * library.  O = softmax(Q K^T / sqrt(dim)) V, single head.
+ *
+ * Layouts (all row-major, contiguous, device pointers):
+ *   Q   [batch_size, N_latent, dim]
+ *   K,V [batch_size, N_input,  dim]
+ *   out [batch_size, N_latent, dim]  (always fp32)
+ *
+ * The first seven entry points keep the names, argument order and C types of
+ * the reference's kernels.so so that its ctypes bindings
+ * (cuda_wrappers.py:83-175) bind unchanged; cudaStream_t becomes hipStream_t
+ * (both opaque pointers; NULL is the null stream).
+ *
+ * Error behaviour: launchers return void, never synchronise and never
+ * allocate caller-visible memory.  A launch the hardware rejects is reported
+ * through hipGetLastError() as in the reference.  In addition, arguments a
+ * kernel cannot run with (dim other than the kernel's supported dim, negative
+ * sizes, num_splits < 1, NULL data pointers with non-zero sizes) are refused
+ * before anything is launched and recorded for xattn_get_last_error().
+ */
+#ifndef XATTN_H
+#define XATTN_H
+
+#include <stdint.h>
+#include <hip/hip_runtime_api.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* ---- fp32 ladder ------------------------------------------------------- */
+
+/* Replaces launch_naive_kernel, kernel_naive.cu:68-78.
+ * One thread per output element; any dim >= 1, any N_input. */
+void launch_naive_kernel(const float* Q, const float* K, const float* V,
+                         float* output, int batch_size, int N_latent,
+                         int N_input, int dim, hipStream_t stream);
+
+/* Replaces launch_parallel_kernel, kernel_warp_parallel.cu:113-123.
+ * One 64-lane wavefront per latent; the full score row lives in LDS,
+ * (4 * N_input + 4) * 4 bytes per workgroup.  dim <= 768, dim % 4 == 0. */
+void launch_parallel_kernel(const float* Q, const float* K, const float* V,
+                            float* output, int batch_size, int N_latent,
+                            int N_input, int dim, hipStream_t stream);
+
+/* Replaces launch_tiled_kernel, kernel_tiled.cu:169-179.
+ * 16-key K tiles staged in LDS, online softmax.  dim <= 768, dim % 4 == 0. */
+void launch_tiled_kernel(const float* Q, const float* K, const float* V,
+                         float* output, int batch_size, int N_latent,
+                         int N_input, int dim, hipStream_t stream);
+
+/* Replaces launch_optimized_kernel, kernel_vectorized.cu:198-208 (the
+ * 'vectorized' entry of cuda_wrappers.py:352-357).  Both GEMMs on fp32 MFMA
+ * (v_mfma_f32_16x16x4_f32), online softmax in registers.  dim == 768.
+ * When batch_size * ceil(N_latent / 64) cannot fill the device it splits the
+ * keys internally and merges with a log-sum-exp pass; the partials then live
+ * in a library-owned device workspace that is allocated on first need and
+ * grown (never shrunk) per device. */
+void launch_optimized_kernel(const float* Q, const float* K, const float* V,
+                             float* output, int batch_size, int N_latent,
+                             int N_input, int dim, hipStream_t stream);
+
+/* ---- split-K (key-parallel) fp32 -------------------------------------- */
+
+/* Replaces launch_splitk_kernel, kernel_splitk.cu:238-251.
+ * Split s covers keys [s*chunk, min((s+1)*chunk, N_input)) with
+ * chunk = ceil(N_input / num_splits).  Caller-owned scratch:
+ *   po [batch_size, N_latent, num_splits, dim]  sum exp(s - pm) * V
+ *   pm [batch_size, N_latent, num_splits]       max score of the split
+ *   pl [batch_size, N_latent, num_splits]       sum exp(s - pm)
+ * An empty split holds (pm, pl, po) = (-FLT_MAX, 0, 0).  dim == 768. */
+void launch_splitk_kernel(const float* Q, const float* K, const float* V,
+                          float* output, float* po, float* pm, float* pl,
+                          int batch_size, int N_latent, int N_input, int dim,
+                          int num_splits, hipStream_t stream);
+
+/* ---- fp16 / bf16 MFMA (fp32 accumulate, fp32 softmax, fp32 output) ----- */
+
+/* Replaces launch_wmma_kernel, kernel_wmma.cu:139-154.  Q, K, V are IEEE
+ * binary16 bit patterns; Q is pre-scaled by 1/sqrt(dim) by the caller
+ * (cuda_wrappers.py:635-640).  dim == 768. */
+void launch_wmma_kernel(const uint16_t* Q, const uint16_t* K,
+                        const uint16_t* V, float* output, int batch_size,
+                        int N_latent, int N_input, int dim,
+                        hipStream_t stream);
+
+/* Replaces launch_wmma_splitk_kernel, kernel_wmma_splitk.cu:201-219.
+ * fp16 inputs as launch_wmma_kernel; splits as launch_splitk_kernel except
+ * that chunk is rounded up to a multiple of 16 (kernel_wmma_splitk.cu:52). */
+void launch_wmma_splitk_kernel(const uint16_t* Q, const uint16_t* K,
+                               const uint16_t* V, float* output, float* po,
+                               float* pm, float* pl, int batch_size,
+                               int N_latent, int N_input, int dim,
+                               int num_splits, hipStream_t stream);
+
+/* Additive (no reference counterpart): bfloat16 twins of the two entry
+ * points above, same contract with bf16 bit patterns for Q, K, V. */
+void launch_wmma_bf16_kernel(const uint16_t* Q, const uint16_t* K,
+                             const uint16_t* V, float* output, int batch_size,
+                             int N_latent, int N_input, int dim,
+                             hipStream_t stream);
+void launch_wmma_splitk_bf16_kernel(const uint16_t* Q, const uint16_t* K,
+                                    const uint16_t* V, float* output,
+                                    float* po, float* pm, float* pl,
+                                    int batch_size, int N_latent, int N_input,
+                                    int dim, int num_splits,
+                                    hipStream_t stream);
+
+/* ---- library status / device queries (additive) ----------------------- */
+
+enum {
+    XATTN_OK = 0,
+    XATTN_ERR_INVALID_VALUE = 1, /* negative size, NULL pointer, bad splits */
+    XATTN_ERR_UNSUPPORTED = 2,   /* shape the kernel is not built for      */
+    XATTN_ERR_LAUNCH = 3,        /* the HIP runtime rejected the launch     */
+    XATTN_ERR_ALLOC = 4          /* workspace allocation failed             */
+};
+
+/* Returns the first error recorded on this host thread since the last call,
+ * and clears it (like hipGetLastError). */
+int xattn_get_last_error(void);
+/* Message of the most recent recorded error ("" if none). */
+const char* xattn_get_last_error_string(void);
+
+/* Replaces the ordinal-based cudaDeviceGetAttribute query of
+ * cuda_wrappers.py:187-194: compute-unit count and maximum LDS bytes one
+ * workgroup may use.  Returns a hipError_t value (0 on success). */
+int xattn_device_info(int device, int* cu_count, int* lds_bytes_per_block);
+
+/* Host copies of the launch planning, for inspection and tests. */
+int xattn_xcd_remap(int block, int num_blocks);
+/* Number of key splits launch_optimized_kernel uses internally. */
+int xattn_optimized_num_splits(int batch_size, int N_latent, int N_input,
+                               int cu_count);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* XATTN_H */

@@ -1,0 +1,140 @@
+"""CPU tests of the C ABI and the host logic of the drop-in wrapper.
+
+No kernel runs here: these cover that kernels.so loads and exports every
+symbol include/xattn.h declares, the launch-planning helpers, argument
+validation (refused before any HIP call), and the wrapper's pure-Python
+policy (choose_num_splits, DesignLimited thresholds, _prep broadcasting).
+"""
+
+import ctypes
+import os
+import re
+
+import numpy as np
+import pytest
+
+from conftest import PKG, ROOT
+
+
+def _declared_symbols():
+    text = open(os.path.join(ROOT, "include", "xattn.h")).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b((?:launch|xattn)_\w+)\s*\(", text)))
+
+
+def test_header_declares_reference_entry_points():
+    names = _declared_symbols()
+    # the seven launchers of the reference's kernels.so (cuda_wrappers.py:83-175)
+    for n in ("launch_naive_kernel", "launch_parallel_kernel", "launch_tiled_kernel",
+              "launch_optimized_kernel", "launch_wmma_kernel", "launch_splitk_kernel",
+              "launch_wmma_splitk_kernel"):
+        assert n in names
+
+
+def test_library_exports_every_declared_symbol(cw):
+    lib = ctypes.CDLL(os.path.join(PKG, "kernels.so"))
+    missing = [n for n in _declared_symbols() if not hasattr(lib, n)]
+    assert not missing, f"kernels.so lacks {missing}"
+
+
+def test_wrapper_flags(cw):
+    assert cw.HAS_SPLITK
+    assert set(cw.LAUNCHERS) == {"naive", "warp", "tiled", "vectorized"}
+    assert cw.cudart.cudaMalloc is cw.cudart.hipMalloc
+
+
+def test_xcd_remap_is_bijection(cw):
+    for n in (1, 7, 8, 9, 64, 255, 256, 257, 512, 1000):
+        got = sorted(cw.lib.xattn_xcd_remap(b, n) for b in range(n))
+        assert got == list(range(n)), n
+    # blocks dealt to one XCD (b % 8 == x) get consecutive logical ids
+    n = 512
+    for x in range(8):
+        ids = [cw.lib.xattn_xcd_remap(b, n) for b in range(x, n, 8)]
+        assert ids == list(range(ids[0], ids[0] + len(ids)))
+
+
+def test_optimized_num_splits(cw):
+    f = cw.lib.xattn_optimized_num_splits
+    assert f(32, 1024, 784, 256) == 1      # 512 workgroups already fill 256 CUs
+    assert f(1, 64, 784, 256) == 49        # one workgroup: one 16-key tile per split
+    assert f(4, 1024, 784, 256) == 4
+    assert f(1, 256, 50176, 256) == 64
+    assert f(1, 64, 0, 256) == 1
+    for b, nl, ni in [(1, 1, 1), (2, 100, 33), (1, 64, 17), (3, 7, 5000)]:
+        s = f(b, nl, ni, 256)
+        tiles = (ni + 15) // 16
+        assert 1 <= s <= tiles
+        chunk_tiles = -(-tiles // s)
+        assert -(-tiles // chunk_tiles) == s  # tile-aligned chunks leave no empty split
+
+
+def test_choose_num_splits_known_values(cw):
+    # values worked out by hand from cuda_wrappers.py:456-467
+    assert cw.choose_num_splits(256, 4096, 1) == 8            # sm 142, lpb 4
+    assert cw.choose_num_splits(256, 4096, 1, sm_count=256) == 16
+    assert cw.choose_num_splits(256, 4096, 1, latents_per_block=16) == 35
+    assert cw.choose_num_splits(256, 4096, 1, sm_count=256, latents_per_block=16) == 64
+    assert cw.choose_num_splits(1024, 784, 32) == 1            # headline
+    assert cw.choose_num_splits(64, 8, 1) == 1                 # N_input // 16 == 0 -> 1
+
+
+def test_warp_design_limit(cw, monkeypatch):
+    monkeypatch.setattr(cw, "_max_smem_optin", lambda device=0: 160 * 1024)
+    assert cw.warp_smem_bytes(10239) <= 160 * 1024 < cw.warp_smem_bytes(10240)
+    q = np.zeros((1, 4, 768), np.float32)
+    k = np.zeros((1, 10240, 768), np.float32)
+    with pytest.raises(cw.DesignLimited):
+        cw.run_warp_parallel_kernel(q, k, k, 4, 10240, 768)
+    with pytest.raises(cw.DesignLimited):
+        cw.benchmark_kernel_events("warp", q, k, k, 1, 4, 10240, 768)
+
+
+def test_mfma_paths_refuse_other_dims(cw):
+    q = np.zeros((1, 4, 64), np.float32)
+    with pytest.raises(cw.DesignLimited):
+        cw.run_vectorized_kernel(q, q, q, 4, 4, 64)
+    with pytest.raises(cw.DesignLimited):
+        cw.benchmark_splitk_events(q, q, q, 1, 4, 4, 64)
+
+
+def test_prep_broadcasting(cw):
+    a = np.arange(2 * 3, dtype=np.float64).reshape(2, 3)
+    got = cw._prep(a, 4)
+    assert got.dtype == np.float32 and got.flags.c_contiguous and got.shape == (4, 2, 3)
+    assert np.array_equal(got, np.repeat(a[None].astype(np.float32), 4, axis=0))
+    b3 = np.ones((3, 2, 3))
+    assert cw._prep(b3, 3).shape == (3, 2, 3)
+
+
+def _call(cw, name, *args):
+    fn = getattr(cw.lib, name)
+    fn(*args)
+    return cw.lib.xattn_get_last_error(), cw.lib.xattn_get_last_error_string().decode()
+
+
+def test_validation_refuses_before_launch(cw):
+    """Refused arguments never reach the HIP runtime (no GPU is needed)."""
+    F = ctypes.POINTER(ctypes.c_float)
+    dummy = ctypes.cast(ctypes.c_void_p(0x1000), F)
+    null = ctypes.cast(ctypes.c_void_p(0), F)
+    s0 = ctypes.c_void_p(0)
+    code, msg = _call(cw, "launch_optimized_kernel", dummy, dummy, dummy, dummy, 1, 64, 784,
+                      100, s0)
+    assert code == 2 and "dim=100" in msg
+    code, msg = _call(cw, "launch_optimized_kernel", dummy, dummy, dummy, dummy, -1, 64, 784,
+                      768, s0)
+    assert code == 1 and "negative" in msg
+    code, msg = _call(cw, "launch_optimized_kernel", null, dummy, dummy, dummy, 1, 64, 784,
+                      768, s0)
+    assert code == 1 and "NULL" in msg
+    code, msg = _call(cw, "launch_splitk_kernel", dummy, dummy, dummy, dummy, dummy, dummy,
+                      dummy, 1, 64, 784, 768, 0, s0)
+    assert code == 1 and "num_splits" in msg
+    code, msg = _call(cw, "launch_tiled_kernel", dummy, dummy, dummy, dummy, 1, 4, 4, 769, s0)
+    assert code == 2
+    # the error is cleared once read
+    assert cw.lib.xattn_get_last_error() == 0
+    # empty problems are a no-op, not an error
+    code, _ = _call(cw, "launch_optimized_kernel", null, null, null, null, 0, 0, 0, 768, s0)
+    assert code == 0

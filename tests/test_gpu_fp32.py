@@ -1,0 +1,164 @@
+"""GPU parity of the fp32 entry points against the float64 oracle.
+
+Gate (written here, from the build's correctness contract): max-abs <= 1e-4
+and rel = max-abs / (max|ref| + 1e-6) <= 1e-3 (the rel definition of
+experiments/bench_perceiver_ni.py:147-148).  Every case calls the HIP library
+through its C ABI (cuda_wrappers -> kernels.so).
+"""
+
+import numpy as np
+import pytest
+
+from conftest import fp32_gate
+
+pytestmark = pytest.mark.gpu
+
+
+def _events(cw, impl, q, k, v):
+    b, nl, d = q.shape
+    out, _, _ = cw.benchmark_kernel_events(impl, q, k, v, b, nl, k.shape[1], d, warmup=1,
+                                           iters=1)
+    return out
+
+
+# ---------------------------------------------------------------------------
+# MFMA kernel (launch_optimized_kernel, the 'vectorized' impl)
+# ---------------------------------------------------------------------------
+
+def test_cfg1_matches_oracle_and_golden(cw, oracle):
+    import os
+    q, k, v = oracle.make_inputs(1, 64, 784, 768, seed=0)
+    out = cw.run_vectorized_kernel(q[0], k[0], v[0], 64, 784, 768)
+    fp32_gate(out, oracle.attention_f64(q, k, v))
+    g = np.load(os.path.join(os.path.dirname(__file__), "golden", "cfg1_seed0.npz"))
+    fp32_gate(out, g["out"])
+
+
+def test_headline_shape_and_determinism(cw, oracle):
+    q, k, v = oracle.make_inputs(32, 1024, 784, 768, seed=1)
+    out1 = _events(cw, "vectorized", q, k, v)
+    fp32_gate(out1, oracle.attention_f64(q, k, v))
+    out2 = _events(cw, "vectorized", q, k, v)
+    assert np.array_equal(out1, out2), "two launches differ bitwise"
+
+
+@pytest.mark.parametrize("b,nl,ni", [(1, 1, 1), (1, 15, 17), (2, 17, 15), (1, 63, 16),
+                                     (3, 65, 33), (1, 100, 785), (2, 129, 1000),
+                                     (5, 64, 784), (1, 1024, 3)])
+def test_edge_shapes(cw, oracle, b, nl, ni):
+    q, k, v = oracle.make_inputs(b, nl, ni, 768, seed=b * 1000 + nl + ni)
+    fp32_gate(_events(cw, "vectorized", q, k, v), oracle.attention_f64(q, k, v))
+
+
+def test_empty_key_set_gives_zeros(cw, oracle):
+    q, _, _ = oracle.make_inputs(2, 70, 1, 768, seed=4)
+    k = np.zeros((2, 0, 768), np.float32)
+    out = _events(cw, "vectorized", q, k, k)
+    assert out.shape == (2, 70, 768) and np.all(out == 0)
+
+
+def test_config2_legacy_seed42_sweep(cw, oracle):
+    for nl in (64, 128, 256, 512, 1024):
+        q, k, v = oracle.make_inputs_legacy(1, nl, 784, 768, seed=42)
+        fp32_gate(cw.run_vectorized_kernel(q[0], k[0], v[0], nl, 784, 768),
+                  oracle.attention_f64(q, k, v))
+
+
+@pytest.mark.parametrize("b", [4, 8, 16, 32])
+def test_config3_batched_sweep(cw, oracle, b):
+    for nl in (64, 128, 256, 512, 1024):
+        q, k, v = oracle.make_inputs_legacy(b, nl, 784, 768, seed=42)
+        fp32_gate(_events(cw, "vectorized", q, k, v), oracle.attention_f64(q, k, v))
+
+
+def test_growing_scores_force_rescales(cw, oracle):
+    """Scores rise by ~12 per key across the key axis, so the running max grows
+    far past the lazy-rescale threshold many times within one row."""
+    rng = np.random.RandomState(8)
+    nl, ni = 40, 200
+    u = rng.randn(768)
+    u /= np.linalg.norm(u)
+    q = np.empty((1, nl, 768), np.float32)
+    q[0] = (u * np.sqrt(768.0) * (1.0 + 0.01 * rng.randn(nl, 1)) + 0.1 * rng.randn(nl, 768))
+    # raw dot q.k_j ~ 12 j, i.e. the score grows by 12/sqrt(768) = 0.43 per key
+    k = (np.arange(ni)[:, None] * (12.0 / np.sqrt(768.0)) * u
+         + 0.05 * rng.randn(ni, 768))[None].astype(np.float32)
+    k = k[:, rng.permutation(ni)]  # rescales happen in every order
+    v = rng.randn(1, ni, 768).astype(np.float32)
+    ref = oracle.attention_f64(q, k, v)
+    fp32_gate(_events(cw, "vectorized", q, k, v), ref)
+    k_sorted = k[:, np.argsort(k[0] @ u)]
+    v_sorted = v[:, np.argsort(k[0] @ u)]
+    fp32_gate(_events(cw, "vectorized", q, k_sorted, v_sorted), ref)
+
+
+def test_special_cases(cw, oracle):
+    q, k, v = oracle.make_inputs(2, 33, 50, 768, seed=12)
+    ones = np.ones_like(v)
+    out = _events(cw, "vectorized", q, k, ones)
+    assert np.max(np.abs(out - 1.0)) < 2e-6
+    out = _events(cw, "vectorized", q, np.zeros_like(k), v)
+    assert np.max(np.abs(out - v.mean(axis=1, keepdims=True))) < 1e-5
+
+
+# ---------------------------------------------------------------------------
+# split-K (launch_splitk_kernel): output and the caller-visible partials
+# ---------------------------------------------------------------------------
+
+@pytest.mark.parametrize("s", [1, 3, 8, 19, 64, 100])
+def test_splitk_output_and_partials(cw, oracle, s):
+    b, nl, ni = 2, 70, 300
+    q, k, v = oracle.make_inputs(b, nl, ni, 768, seed=s)
+    out, (po, pm, pl) = cw.splitk_partials(q, k, v, b, nl, ni, 768, s)
+    fp32_gate(out, oracle.attention_f64(q, k, v))
+    rpo, rpm, rpl = oracle.splitk_partials(q, k, v, s)
+    live = rpm > -oracle.FLT_MAX
+    assert np.array_equal(pm[~live], np.full((~live).sum(), -oracle.FLT_MAX, np.float32))
+    assert np.all(pl[~live] == 0) and np.all(po[~live] == 0)
+    assert np.max(np.abs(pm[live] - rpm[live])) < 1e-5
+    assert np.max(np.abs(pl[live] - rpl[live]) / rpl[live]) < 1e-5
+    fp32_gate(po[live] / pl[live][:, None], rpo[live] / rpl[live][:, None])
+
+
+def test_splitk_golden(cw, oracle):
+    import os
+    g = np.load(os.path.join(os.path.dirname(__file__), "golden", "splitk_small.npz"))
+    b, nl, ni, d, s = [int(x) for x in g["shape"]]
+    q, k, v = oracle.make_inputs(b, nl, ni, d, seed=3)
+    out, (po, pm, pl) = cw.splitk_partials(q, k, v, b, nl, ni, d, s)
+    fp32_gate(out, g["out"])
+    fp32_gate(po, g["po"])
+    assert np.allclose(pm, g["pm"], atol=1e-5) and np.allclose(pl, g["pl"], rtol=1e-5)
+
+
+@pytest.mark.parametrize("ni", [4096, 16384, 50176])
+def test_config4_long_input(cw, oracle, ni):
+    cu, _ = cw.device_info()
+    q, k, v = oracle.make_inputs(1, 256, ni, 768, seed=ni, q_std=0.02)
+    out, _, _, s = cw.benchmark_splitk_events(q, k, v, 1, 256, ni, 768, warmup=1, iters=1,
+                                              sm_count=cu)
+    assert s > 1
+    fp32_gate(out, oracle.attention_f64(q, k, v))
+    fp32_gate(_events(cw, "vectorized", q, k, v), oracle.attention_f64(q, k, v))
+
+
+# ---------------------------------------------------------------------------
+# ladder rungs
+# ---------------------------------------------------------------------------
+
+@pytest.mark.parametrize("impl", ["naive", "warp", "tiled"])
+@pytest.mark.parametrize("b,nl,ni,d", [(2, 9, 50, 768), (1, 5, 33, 64), (1, 7, 17, 100),
+                                       (1, 4, 0, 768)])
+def test_rungs(cw, oracle, impl, b, nl, ni, d):
+    q, k, v = oracle.make_inputs(b, nl, ni, d, seed=nl * ni + d)
+    out = _events(cw, impl, q, k, v)
+    fp32_gate(out, oracle.attention_f64(q, k, v))
+
+
+@pytest.mark.parametrize("fn", ["run_naive_kernel", "run_warp_parallel_kernel",
+                                "run_tiled_kernel", "run_vectorized_kernel"])
+def test_legacy_drivers_2d_inputs(cw, oracle, fn):
+    q, k, v = oracle.make_inputs_legacy(1, 64, 784, 768, seed=42)
+    out = getattr(cw, fn)(q[0], k[0], v[0], 64, 784, 768)
+    assert out.shape == (1, 64, 768)
+    fp32_gate(out, oracle.attention_f64(q, k, v))
