@@ -7,6 +7,8 @@ kernels.so).  One step = one call over the whole batch; inputs are resident in
 HBM before timing starts.  Prints one JSON line.
 
     python bench.py [--gpus 1] [--steps 200] [--warmup 20] [--cpu-seconds 10]
+    python bench.py --case cfg5-bf16      # other workloads (profiling; no CPU leg)
+    python bench.py --copy-calibration 1024   # D2D copy of 1 GiB, for HBM counters
 
 Algorithmic work per call: FLOP = 4*B*NL*NI*D = 78.92 GFLOP; bytes =
 B*(NL*D + 2*NI*D)*4 + B*NL*D*4 = 355.5 MB.
@@ -80,6 +82,117 @@ def cpu_baseline(seconds):
     }
 
 
+# Secondary workloads (split-K long input, 16-bit, small batch): name ->
+# (B, NL, NI, element type, entry point, Q std)
+CASES = {
+    "cfg1": (1, 64, 784, "fp32", "launch_optimized_kernel", 1.0),
+    "cfg4-splitk-4096": (1, 256, 4096, "fp32", "launch_splitk_kernel", 0.02),
+    "cfg4-splitk-16384": (1, 256, 16384, "fp32", "launch_splitk_kernel", 0.02),
+    "cfg4-splitk-50176": (1, 256, 50176, "fp32", "launch_splitk_kernel", 0.02),
+    "cfg5-fp16": (16, 512, 784, "fp16", "launch_wmma_kernel", 1.0),
+    "cfg5-bf16": (16, 512, 784, "bf16", "launch_wmma_bf16_kernel", 1.0),
+    "headline-bf16": (32, 1024, 784, "bf16", "launch_wmma_bf16_kernel", 1.0),
+}
+
+
+def time_launches(cw, launch, steps, warmup):
+    """warmup launches, then `steps` launches each bracketed by HIP events on
+    the launch stream (the null stream); returns (wall_s, per-launch ms)."""
+    stream = ctypes.c_void_p(0)
+    launch()
+    cw._lib_error_check("launch")
+    for _ in range(warmup):
+        launch()
+    if cw.cudart.cudaDeviceSynchronize() != 0:
+        raise RuntimeError("warmup failed")
+    evs = [(ctypes.c_void_p(), ctypes.c_void_p()) for _ in range(steps)]
+    for a, b in evs:
+        cw.cudart.cudaEventCreate(ctypes.byref(a))
+        cw.cudart.cudaEventCreate(ctypes.byref(b))
+    cw.cudart.cudaDeviceSynchronize()
+    t0 = time.perf_counter()
+    for a, b in evs:
+        cw.cudart.cudaEventRecord(a, stream)
+        launch()
+        cw.cudart.cudaEventRecord(b, stream)
+    cw.cudart.cudaDeviceSynchronize()
+    wall = time.perf_counter() - t0
+    ms = ctypes.c_float()
+    per = []
+    for a, b in evs:
+        cw.cudart.cudaEventElapsedTime(ctypes.byref(ms), a, b)
+        per.append(ms.value)
+        cw.cudart.cudaEventDestroy(a)
+        cw.cudart.cudaEventDestroy(b)
+    cw._lib_error_check("launch")
+    return wall, per
+
+
+def run_case(cw, name, steps, warmup):
+    b, nl, ni, et, entry, q_std = CASES[name]
+    cu, _ = cw.device_info()
+    rng = np.random.RandomState(0)
+    q = (rng.randn(b, nl, D) * q_std).astype(np.float32)
+    k = rng.randn(b, ni, D).astype(np.float32)
+    v = rng.randn(b, ni, D).astype(np.float32)
+    if et == "fp32":
+        host = (q, k, v)
+    else:
+        host = cw._half_inputs(q, k, v, b, D, bf16=(et == "bf16"))
+    bufs = [cw._allocate_gpu_memory(a.nbytes) for a in host]
+    for a, p in zip(host, bufs):
+        cw._copy_to_gpu(a, p, a.nbytes)
+    out = cw._allocate_gpu_memory(b * nl * D * 4)
+    extra = []
+    stream = ctypes.c_void_p(0)
+    fn = getattr(cw.lib, entry)
+    note = {}
+    if entry == "launch_splitk_kernel":
+        s = cw.choose_num_splits(nl, ni, b, sm_count=cu)
+        extra = [cw._allocate_gpu_memory(b * nl * s * D * 4),
+                 cw._allocate_gpu_memory(b * nl * s * 4), cw._allocate_gpu_memory(b * nl * s * 4)]
+        note["num_splits"] = s
+        args = [cw._fptr(p) for p in bufs + [out] + extra] + [b, nl, ni, D, s, stream]
+    elif et == "fp32":
+        args = [cw._fptr(p) for p in bufs + [out]] + [b, nl, ni, D, stream]
+    else:
+        args = bufs + [cw._fptr(out), b, nl, ni, D, stream]
+    wall, per = time_launches(cw, lambda: fn(*args), steps, warmup)
+    for p in bufs + [out] + extra:
+        cw._free_gpu_memory(p)
+    bpe = 4 if et == "fp32" else 2
+    kern_ms = float(np.mean(per))
+    flop = algorithmic_flop(b, nl, ni, D)
+    byt = algorithmic_bytes(b, nl, ni, D, bpe)
+    peak = PEAK_FP32_MFMA_TFLOPS if et == "fp32" else 2516.6
+    return {
+        "case": name, "entry_point": entry, "dtype": et, "B": b, "NL": nl, "NI": ni, "D": D,
+        "us_per_call": round(kern_ms * 1e3, 2),
+        "tflops": round(flop / (kern_ms * 1e-3) / 1e12, 3),
+        "pct_of_mfma_peak": round(100 * flop / (kern_ms * 1e-3) / 1e12 / peak, 2),
+        "gbs_algorithmic": round(byt / (kern_ms * 1e-3) / 1e9, 1),
+        "pct_of_hbm_peak": round(100 * byt / (kern_ms * 1e-3) / 8.0e12, 2),
+        "ms_per_step_wall": round(wall * 1e3 / steps, 5), **note,
+    }
+
+
+def copy_calibration(cw, mib, reps=5):
+    """Plain device-to-device copy of `mib` MiB, `reps` times: reads and writes
+    exactly mib MiB per copy, the reference point for FETCH_SIZE/WRITE_SIZE."""
+    n = mib * 1024 * 1024
+    a = cw._allocate_gpu_memory(n)
+    b = cw._allocate_gpu_memory(n)
+    cw.cudart.cudaMemset(a, 1, n)
+    cw.cudart.cudaDeviceSynchronize()
+    for _ in range(reps):
+        if cw.cudart.hipMemcpy(b, a, n, 3) != 0:  # hipMemcpyDeviceToDevice
+            raise RuntimeError("hipMemcpy D2D failed")
+    cw.cudart.cudaDeviceSynchronize()
+    cw._free_gpu_memory(a)
+    cw._free_gpu_memory(b)
+    print(json.dumps({"copy_calibration_bytes_per_copy": n, "copies": reps}), flush=True)
+
+
 def main():
     ap = argparse.ArgumentParser(description=__doc__.splitlines()[0])
     ap.add_argument("--gpus", type=int, default=1)
@@ -87,6 +200,9 @@ def main():
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
+    ap.add_argument("--case", choices=sorted(CASES), action="append",
+                    help="run a secondary workload instead of the headline")
+    ap.add_argument("--copy-calibration", type=int, metavar="MIB")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU: this build has no multi-GPU path "
@@ -94,6 +210,14 @@ def main():
         sys.exit(2)
 
     import cuda_wrappers as cw
+
+    if args.copy_calibration:
+        copy_calibration(cw, args.copy_calibration)
+        return
+    if args.case:
+        for name in args.case:
+            print(json.dumps(run_case(cw, name, args.steps, args.warmup)), flush=True)
+        return
 
     cu, _ = cw.device_info()
     rng = np.random.RandomState(0)
@@ -113,35 +237,9 @@ def main():
     def launch():
         cw.lib.launch_optimized_kernel(qp, kp, vp, op, B, NL, NI, D, stream)
 
-    launch()
-    cw._lib_error_check("launch_optimized_kernel")
-    for _ in range(args.warmup):
-        launch()
-    if cw.cudart.cudaDeviceSynchronize() != 0:
-        raise RuntimeError("warmup failed")
-
     # Timed region: K back-to-back launches bracketed by a device sync; each
     # launch also bracketed by HIP events on the launch stream.
-    evs = [(ctypes.c_void_p(), ctypes.c_void_p()) for _ in range(args.steps)]
-    for a, b in evs:
-        cw.cudart.cudaEventCreate(ctypes.byref(a))
-        cw.cudart.cudaEventCreate(ctypes.byref(b))
-    cw.cudart.cudaDeviceSynchronize()
-    t0 = time.perf_counter()
-    for a, b in evs:
-        cw.cudart.cudaEventRecord(a, stream)
-        launch()
-        cw.cudart.cudaEventRecord(b, stream)
-    cw.cudart.cudaDeviceSynchronize()
-    wall = time.perf_counter() - t0
-    ms = ctypes.c_float()
-    per = []
-    for a, b in evs:
-        cw.cudart.cudaEventElapsedTime(ctypes.byref(ms), a, b)
-        per.append(ms.value)
-        cw.cudart.cudaEventDestroy(a)
-        cw.cudart.cudaEventDestroy(b)
-    cw._lib_error_check("launch_optimized_kernel")
+    wall, per = time_launches(cw, launch, args.steps, args.warmup)
 
     flop = algorithmic_flop(B, NL, NI, D)
     ms_per_step = wall * 1e3 / args.steps

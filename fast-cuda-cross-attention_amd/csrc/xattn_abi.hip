@@ -150,17 +150,42 @@ bool validate_splits(const char* who, const void* po, const void* pm, const void
     return true;
 }
 
-int optimized_num_splits(int B, int NL, int NI, int cu) {
+// Key splits that let B * row_blocks workgroups fill `cu` compute units, with
+// every split a whole number of `tile`-key tiles.
+int plan_splits(int B, int NL, int NI, int cu, int bm, int tile) {
     if (B <= 0 || NL <= 0 || NI <= 0) return 1;
-    const long long items = (long long)B * f32_row_blocks(NL);
+    const long long items = (long long)B * ((NL + bm - 1) / bm);
     if (items >= cu) return 1;
-    const int tiles = (NI + 15) / 16;
+    const int tiles = (NI + tile - 1) / tile;
     long long s = (cu + items - 1) / items;
     if (s > tiles) s = tiles;
     if (s < 1) s = 1;
     // tile-aligned chunks: recompute the count that chunk implies
     const int chunk_tiles = (int)((tiles + s - 1) / s);
     return (tiles + chunk_tiles - 1) / chunk_tiles;
+}
+
+int optimized_num_splits(int B, int NL, int NI, int cu) {
+    return plan_splits(B, NL, NI, cu, 64, 16);
+}
+
+// Library-workspace split launch shared by the fp32 and 16-bit entry points.
+struct SplitScratch {
+    float* po;
+    float* pm;
+    float* pl;
+};
+
+static bool split_scratch(SplitScratch* s, int B, int NL, int S) {
+    const size_t rows = (size_t)B * NL;
+    const size_t po_bytes = rows * S * kDim * sizeof(float);
+    const size_t ml_bytes = rows * S * sizeof(float);
+    char* ws = (char*)workspace(po_bytes + 2 * ml_bytes + 256);
+    if (!ws) return false;
+    s->po = (float*)ws;
+    s->pm = (float*)(ws + po_bytes);
+    s->pl = (float*)(ws + po_bytes + ml_bytes);
+    return true;
 }
 
 }  // namespace xattn
@@ -252,18 +277,12 @@ void launch_optimized_kernel(const float* Q, const float* K, const float* V, flo
     }
     const int tiles = (N_input + 15) / 16;
     const int chunk = ((tiles + S - 1) / S) * 16;
-    const size_t rows = (size_t)batch_size * N_latent;
-    const size_t po_bytes = rows * S * kDim * sizeof(float);
-    const size_t ml_bytes = rows * S * sizeof(float);
-    char* ws = (char*)workspace(po_bytes + 2 * ml_bytes + 256);
-    if (!ws) return;
-    float* po = (float*)ws;
-    float* pm = (float*)(ws + po_bytes);
-    float* pl = (float*)(ws + po_bytes + ml_bytes);
-    if (!launch_flash_f32(Q, K, V, nullptr, po, pm, pl, batch_size, N_latent, N_input, S, chunk,
-                          stream))
+    SplitScratch sc;
+    if (!split_scratch(&sc, batch_size, N_latent, S)) return;
+    if (!launch_flash_f32(Q, K, V, nullptr, sc.po, sc.pm, sc.pl, batch_size, N_latent, N_input,
+                          S, chunk, stream))
         return;
-    launch_lse_combine(po, pm, pl, output, (int)rows, S, stream);
+    launch_lse_combine(sc.po, sc.pm, sc.pl, output, batch_size * N_latent, S, stream);
 }
 
 void launch_splitk_kernel(const float* Q, const float* K, const float* V, float* output,
@@ -284,6 +303,79 @@ void launch_splitk_kernel(const float* Q, const float* K, const float* V, float*
                           num_splits, chunk, stream))
         return;
     launch_lse_combine(po, pm, pl, output, batch_size * N_latent, num_splits, stream);
+}
+
+static void wmma_common(bool bf16, const char* who, const uint16_t* Q, const uint16_t* K,
+                        const uint16_t* V, float* output, int batch_size, int N_latent,
+                        int N_input, int dim, hipStream_t stream) {
+    if (!validate_common(who, Q, K, V, output, batch_size, N_latent, N_input, dim)) return;
+    if (!validate_dim768(who, dim)) return;
+    if (batch_size == 0 || N_latent == 0) return;
+    const int S = plan_splits(batch_size, N_latent, N_input, device_cu_count(), 64, 32);
+    if (S <= 1) {
+        launch_flash16(bf16, Q, K, V, output, nullptr, nullptr, nullptr, batch_size, N_latent,
+                       N_input, 1, N_input, stream);
+        return;
+    }
+    const int tiles = (N_input + 31) / 32;
+    const int chunk = ((tiles + S - 1) / S) * 32;
+    SplitScratch sc;
+    if (!split_scratch(&sc, batch_size, N_latent, S)) return;
+    if (!launch_flash16(bf16, Q, K, V, nullptr, sc.po, sc.pm, sc.pl, batch_size, N_latent,
+                        N_input, S, chunk, stream))
+        return;
+    launch_lse_combine(sc.po, sc.pm, sc.pl, output, batch_size * N_latent, S, stream);
+}
+
+static void wmma_splitk_common(bool bf16, const char* who, const uint16_t* Q, const uint16_t* K,
+                               const uint16_t* V, float* output, float* po, float* pm,
+                               float* pl, int batch_size, int N_latent, int N_input, int dim,
+                               int num_splits, hipStream_t stream) {
+    if (!validate_common(who, Q, K, V, output, batch_size, N_latent, N_input, dim)) return;
+    if (!validate_dim768(who, dim)) return;
+    if (!validate_splits(who, po, pm, pl, batch_size, N_latent, num_splits)) return;
+    if (batch_size == 0 || N_latent == 0) return;
+    if ((long long)batch_size * N_latent * num_splits > 0x7fffffffLL) {
+        set_error(XATTN_ERR_INVALID_VALUE, "%s: B*NL*num_splits too large", who);
+        return;
+    }
+    // kernel_wmma_splitk.cu:52: chunk = ceil(NI / S) rounded up to a multiple of 16
+    long long chunk = ((long long)N_input + num_splits - 1) / num_splits;
+    chunk = (chunk + 15) / 16 * 16;
+    if (!launch_flash16(bf16, Q, K, V, nullptr, po, pm, pl, batch_size, N_latent, N_input,
+                        num_splits, (int)chunk, stream))
+        return;
+    launch_lse_combine(po, pm, pl, output, batch_size * N_latent, num_splits, stream);
+}
+
+void launch_wmma_kernel(const uint16_t* Q, const uint16_t* K, const uint16_t* V, float* output,
+                        int batch_size, int N_latent, int N_input, int dim,
+                        hipStream_t stream) {
+    wmma_common(false, "launch_wmma_kernel", Q, K, V, output, batch_size, N_latent, N_input,
+                dim, stream);
+}
+
+void launch_wmma_bf16_kernel(const uint16_t* Q, const uint16_t* K, const uint16_t* V,
+                             float* output, int batch_size, int N_latent, int N_input, int dim,
+                             hipStream_t stream) {
+    wmma_common(true, "launch_wmma_bf16_kernel", Q, K, V, output, batch_size, N_latent,
+                N_input, dim, stream);
+}
+
+void launch_wmma_splitk_kernel(const uint16_t* Q, const uint16_t* K, const uint16_t* V,
+                               float* output, float* po, float* pm, float* pl, int batch_size,
+                               int N_latent, int N_input, int dim, int num_splits,
+                               hipStream_t stream) {
+    wmma_splitk_common(false, "launch_wmma_splitk_kernel", Q, K, V, output, po, pm, pl,
+                       batch_size, N_latent, N_input, dim, num_splits, stream);
+}
+
+void launch_wmma_splitk_bf16_kernel(const uint16_t* Q, const uint16_t* K, const uint16_t* V,
+                                    float* output, float* po, float* pm, float* pl,
+                                    int batch_size, int N_latent, int N_input, int dim,
+                                    int num_splits, hipStream_t stream) {
+    wmma_splitk_common(true, "launch_wmma_splitk_bf16_kernel", Q, K, V, output, po, pm, pl,
+                       batch_size, N_latent, N_input, dim, num_splits, stream);
 }
 
 }  // extern "C"

@@ -8,6 +8,7 @@ namespace xattn {
 int device_cu_count();
 int device_max_lds();
 int optimized_num_splits(int B, int NL, int NI, int cu);
+int plan_splits(int B, int NL, int NI, int cu, int bm, int tile);
 bool validate_common(const char* who, const void* Q, const void* K, const void* V,
                      const void* out, int B, int NL, int NI, int dim);
 bool validate_dim768(const char* who, int dim);
@@ -23,6 +24,12 @@ bool launch_flash_f32(const float* Q, const float* K, const float* V, float* out
                       hipStream_t stream);
 bool launch_lse_combine(const float* po, const float* pm, const float* pl, float* out, int rows,
                         int S, hipStream_t stream);
+
+// fp16 / bf16 MFMA flash kernel; Q/K/V are 16-bit bit patterns, Q pre-scaled
+// by 1/sqrt(768).  Same po semantics as launch_flash_f32.
+bool launch_flash16(bool bf16, const void* Q, const void* K, const void* V, float* out,
+                    float* po, float* pm, float* pl, int B, int NL, int NI, int S, int chunk,
+                    hipStream_t stream);
 
 // fp32 ladder rungs
 bool launch_naive(const float* Q, const float* K, const float* V, float* out, int B, int NL,

@@ -575,3 +575,134 @@ def splitk_partials(Q, K, V, batch_size, N_latent, N_input, D, num_splits):
     out, _, _, parts = _splitk_run(launch, Q, K, V, batch_size, N_latent, N_input, D,
                                    num_splits, 1, 0, "split-K", keep_partials=True)
     return out, parts
+
+
+# ---------------------------------------------------------------------------
+# fp16 / bf16 MFMA paths
+# ---------------------------------------------------------------------------
+
+def _to_bf16_bits(x):
+    """float32 -> bfloat16 bit patterns (uint16), round to nearest even."""
+    u = np.ascontiguousarray(x, np.float32).view(np.uint32).astype(np.uint64)
+    nan = (u & 0x7FFFFFFF) > 0x7F800000
+    rounded = (u + 0x7FFF + ((u >> 16) & 1)) >> 16
+    return np.where(nan, (u >> 16) | 0x40, rounded).astype(np.uint16)
+
+
+def _half_inputs(Q, K, V, batch_size, D, bf16):
+    """Host side of the 16-bit paths: Q pre-scaled by 1/sqrt(D) in fp32, then
+    Q, K, V rounded to fp16 or bf16 (cuda_wrappers.py:635-640)."""
+    Q = _prep(Q, batch_size).astype(np.float32) / np.sqrt(D).astype(np.float32)
+    K = _prep(K, batch_size)
+    V = _prep(V, batch_size)
+    if bf16:
+        return tuple(np.ascontiguousarray(_to_bf16_bits(a)) for a in (Q, K, V))
+    return tuple(np.ascontiguousarray(a, dtype=np.float16) for a in (Q, K, V))
+
+
+def _wmma_events(launch_fn, what, Q, K, V, batch_size, N_latent, N_input, D, warmup, iters,
+                 bf16):
+    _require_dim(D, what)
+    Qh, Kh, Vh = _half_inputs(Q, K, V, batch_size, D, bf16)
+    out_size = batch_size * N_latent * D * 4
+    Q_gpu = _allocate_gpu_memory(Qh.nbytes)
+    K_gpu = _allocate_gpu_memory(Kh.nbytes)
+    V_gpu = _allocate_gpu_memory(Vh.nbytes)
+    out_gpu = _allocate_gpu_memory(out_size)
+    ev = _Events()
+    try:
+        cudart.cudaMemset(out_gpu, 0, max(out_size, 1))
+        _copy_to_gpu(Qh, Q_gpu, Qh.nbytes)
+        _copy_to_gpu(Kh, K_gpu, Kh.nbytes)
+        _copy_to_gpu(Vh, V_gpu, Vh.nbytes)
+        op = _fptr(out_gpu)
+        null_stream = ctypes.c_void_p(0)
+
+        def _launch():
+            launch_fn(Q_gpu, K_gpu, V_gpu, op, batch_size, N_latent, N_input, D, null_stream)
+
+        _warmup(_launch, warmup, f"{what} (Nl={N_latent} Ni={N_input})")
+        times = ev.time(_launch, iters, null_stream)
+        output = np.zeros((batch_size, N_latent, D), dtype=np.float32)
+        _copy_from_gpu(out_gpu, output, out_size)
+        mean_ms, std_ms = _stats(times)
+        return output, mean_ms, std_ms
+    finally:
+        ev.destroy()
+        for p in (Q_gpu, K_gpu, V_gpu, out_gpu):
+            _free_gpu_memory(p)
+
+
+def benchmark_wmma_events(Q, K, V, batch_size, N_latent, N_input, D,
+                          warmup=20, iters=100):
+    """HIP-event timing for the fp16 MFMA kernel.
+
+    Takes fp32 Q/K/V (same references the other kernels use), pre-scales Q by
+    1/sqrt(D), casts to fp16, runs the MFMA kernel, and returns (fp32 output,
+    mean_ms, std_ms).
+    """
+    if not HAS_WMMA:
+        raise RuntimeError("kernels.so has no launch_wmma_kernel (rebuild with "
+                           "csrc/xattn_flash_f16.hip).")
+    return _wmma_events(lib.launch_wmma_kernel, "fp16 MFMA kernel", Q, K, V, batch_size,
+                        N_latent, N_input, D, warmup, iters, bf16=False)
+
+
+def benchmark_wmma_bf16_events(Q, K, V, batch_size, N_latent, N_input, D,
+                               warmup=20, iters=100):
+    """bf16 twin of ``benchmark_wmma_events`` (additive)."""
+    if not HAS_WMMA_BF16:
+        raise RuntimeError("kernels.so has no launch_wmma_bf16_kernel.")
+    return _wmma_events(lib.launch_wmma_bf16_kernel, "bf16 MFMA kernel", Q, K, V, batch_size,
+                        N_latent, N_input, D, warmup, iters, bf16=True)
+
+
+def _wmma_splitk(launch_fn, what, Q, K, V, batch_size, N_latent, N_input, D, warmup, iters,
+                 num_splits, sm_count, bf16, keep_partials=False):
+    _require_dim(D, what)
+    if num_splits is None:
+        num_splits = choose_num_splits(N_latent, N_input, batch_size, sm_count,
+                                       latents_per_block=16)
+    Qh, Kh, Vh = _half_inputs(Q, K, V, batch_size, D, bf16)
+    launch = lambda q, k, v, *rest: launch_fn(q, k, v, *rest)  # noqa: E731
+    res = _splitk_run(launch, Qh, Kh, Vh, batch_size, N_latent, N_input, D, num_splits,
+                      warmup, iters, what, keep_partials=keep_partials)
+    return res, num_splits
+
+
+def benchmark_wmma_splitk_events(Q, K, V, batch_size, N_latent, N_input, D,
+                                 warmup=20, iters=100, num_splits=None,
+                                 sm_count=142):
+    """HIP-event timing for the fp16 MFMA split-K kernel (fp16 + key-split).
+
+    fp16 Q/K/V (Q pre-scaled by 1/sqrt(D)), fp32 scratch + output.  Returns
+    (fp32 output, mean_ms, std_ms, num_splits).
+    """
+    if not HAS_WMMA_SPLITK:
+        raise RuntimeError("kernels.so has no launch_wmma_splitk_kernel "
+                           "(rebuild with csrc/xattn_flash_f16.hip).")
+    (out, mean_ms, std_ms), s = _wmma_splitk(
+        lib.launch_wmma_splitk_kernel, "fp16 split-K", Q, K, V, batch_size, N_latent,
+        N_input, D, warmup, iters, num_splits, sm_count, bf16=False)
+    return out, mean_ms, std_ms, s
+
+
+def benchmark_wmma_splitk_bf16_events(Q, K, V, batch_size, N_latent, N_input, D,
+                                      warmup=20, iters=100, num_splits=None,
+                                      sm_count=142):
+    """bf16 twin of ``benchmark_wmma_splitk_events`` (additive)."""
+    if not HAS_WMMA_SPLITK_BF16:
+        raise RuntimeError("kernels.so has no launch_wmma_splitk_bf16_kernel.")
+    (out, mean_ms, std_ms), s = _wmma_splitk(
+        lib.launch_wmma_splitk_bf16_kernel, "bf16 split-K", Q, K, V, batch_size, N_latent,
+        N_input, D, warmup, iters, num_splits, sm_count, bf16=True)
+    return out, mean_ms, std_ms, s
+
+
+def wmma_splitk_partials(Q, K, V, batch_size, N_latent, N_input, D, num_splits, bf16=False):
+    """Run the 16-bit split-K once; return (output, (po, pm, pl))."""
+    fn = lib.launch_wmma_splitk_bf16_kernel if bf16 else lib.launch_wmma_splitk_kernel
+    (out, _, _, parts), _ = _wmma_splitk(fn, "16-bit split-K", Q, K, V, batch_size, N_latent,
+                                         N_input, D, 1, 0, num_splits, 142, bf16,
+                                         keep_partials=True)
+    return out, parts

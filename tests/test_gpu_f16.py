@@ -1,0 +1,97 @@
+"""GPU parity of the fp16 / bf16 MFMA entry points.
+
+Gates: rel <= 2e-2 against the fp32 oracle on the unrounded inputs (the
+build's reduced-precision contract), plus a tighter check against the oracle
+evaluated on exactly the rounded inputs the kernel sees, which isolates the
+kernel's own error (P rounded to 16 bits, fp32 accumulation):
+rel <= 4e-3 for bf16 and <= 1e-3 for fp16.
+"""
+
+import math
+
+import numpy as np
+import pytest
+
+pytestmark = pytest.mark.gpu
+
+GATE = 2e-2
+TIGHT = {False: 1e-3, True: 4e-3}
+
+
+def _rounded_ref(oracle, cw, q, k, v, bf16):
+    """float64 attention on the rounded inputs (Q pre-scaled then rounded)."""
+    qh, kh, vh = cw._half_inputs(q, k, v, q.shape[0], q.shape[-1], bf16)
+    if bf16:
+        f = oracle.bf16_bits_to_f32
+        qf, kf, vf = f(qh), f(kh), f(vh)
+    else:
+        qf, kf, vf = (a.astype(np.float32) for a in (qh, kh, vh))
+    return oracle.attention_f64(qf.astype(np.float64) * math.sqrt(q.shape[-1]), kf, vf)
+
+
+def _run(cw, q, k, v, bf16):
+    b, nl, d = q.shape
+    fn = cw.benchmark_wmma_bf16_events if bf16 else cw.benchmark_wmma_events
+    out, _, _ = fn(q, k, v, b, nl, k.shape[1], d, warmup=1, iters=1)
+    return out
+
+
+def _check(oracle, cw, out, q, k, v, bf16):
+    assert np.all(np.isfinite(out))
+    rel = oracle.rel_err(out, oracle.attention_f64(q, k, v))
+    tight = oracle.rel_err(out, _rounded_ref(oracle, cw, q, k, v, bf16))
+    assert rel <= GATE, f"rel vs fp32 oracle {rel:.3e}"
+    assert tight <= TIGHT[bf16], f"rel vs rounded-input oracle {tight:.3e}"
+    return rel, tight
+
+
+@pytest.mark.parametrize("bf16", [False, True], ids=["fp16", "bf16"])
+def test_config5(cw, oracle, bf16):
+    q, k, v = oracle.make_inputs(16, 512, 784, 768, seed=5)
+    _check(oracle, cw, _run(cw, q, k, v, bf16), q, k, v, bf16)
+
+
+@pytest.mark.parametrize("bf16", [False, True], ids=["fp16", "bf16"])
+@pytest.mark.parametrize("b,nl,ni", [(1, 1, 1), (2, 17, 33), (1, 100, 785), (3, 64, 31),
+                                     (1, 65, 64), (1, 64, 784), (32, 1024, 784)])
+def test_shapes(cw, oracle, bf16, b, nl, ni):
+    q, k, v = oracle.make_inputs(b, nl, ni, 768, seed=b + nl + ni)
+    _check(oracle, cw, _run(cw, q, k, v, bf16), q, k, v, bf16)
+
+
+@pytest.mark.parametrize("bf16", [False, True], ids=["fp16", "bf16"])
+def test_empty_keys(cw, oracle, bf16):
+    q, _, _ = oracle.make_inputs(1, 20, 1, 768, seed=1)
+    k = np.zeros((1, 0, 768), np.float32)
+    assert np.all(_run(cw, q, k, k, bf16) == 0)
+
+
+@pytest.mark.parametrize("bf16", [False, True], ids=["fp16", "bf16"])
+@pytest.mark.parametrize("s", [1, 4, 9, 35, 64])
+def test_splitk_partials(cw, oracle, bf16, s):
+    b, nl, ni = 2, 48, 500
+    q, k, v = oracle.make_inputs(b, nl, ni, 768, seed=s)
+    out, (po, pm, pl) = cw.wmma_splitk_partials(q, k, v, b, nl, ni, 768, s, bf16=bf16)
+    _check(oracle, cw, out, q, k, v, bf16)
+    # partials on the rounded inputs, chunk rounded up to 16 keys
+    qh, kh, vh = cw._half_inputs(q, k, v, b, 768, bf16)
+    f = oracle.bf16_bits_to_f32 if bf16 else (lambda a: a.astype(np.float32))
+    rpo, rpm, rpl = oracle.splitk_partials(f(qh).astype(np.float64) * math.sqrt(768), f(kh),
+                                           f(vh), s, align=16)
+    live = rpm > -oracle.FLT_MAX
+    assert np.all(pm[~live] == -oracle.FLT_MAX) and np.all(pl[~live] == 0)
+    assert np.all(po[~live] == 0)
+    assert np.max(np.abs(pm[live] - rpm[live])) < 1e-3  # scores are q.k with Q pre-scaled
+    assert np.max(np.abs(pl[live] / rpl[live] - 1)) < TIGHT[bf16]
+    rel = oracle.rel_err(po[live] / pl[live][:, None], rpo[live] / rpl[live][:, None])
+    assert rel < TIGHT[bf16]
+
+
+@pytest.mark.parametrize("bf16", [False, True], ids=["fp16", "bf16"])
+def test_splitk_long_input(cw, oracle, bf16):
+    cu, _ = cw.device_info()
+    q, k, v = oracle.make_inputs(1, 256, 16384, 768, seed=2, q_std=0.02)
+    fn = cw.benchmark_wmma_splitk_bf16_events if bf16 else cw.benchmark_wmma_splitk_events
+    out, _, _, s = fn(q, k, v, 1, 256, 16384, 768, warmup=1, iters=1, sm_count=cu)
+    assert s > 1
+    _check(oracle, cw, out, q, k, v, bf16)
