@@ -148,7 +148,7 @@ def run_case(cw, name, steps, warmup):
     fn = getattr(cw.lib, entry)
     note = {}
     if entry == "launch_splitk_kernel":
-        s = cw.choose_num_splits(nl, ni, b, sm_count=cu)
+        s = cw.plan_num_splits(nl, ni, b, cu)
         extra = [cw._allocate_gpu_memory(b * nl * s * D * 4),
                  cw._allocate_gpu_memory(b * nl * s * 4), cw._allocate_gpu_memory(b * nl * s * 4)]
         note["num_splits"] = s

@@ -219,6 +219,13 @@ int xattn_optimized_num_splits(int batch_size, int N_latent, int N_input, int cu
     return optimized_num_splits(batch_size, N_latent, N_input, cu_count);
 }
 
+int xattn_plan_splits(int batch_size, int N_latent, int N_input, int cu_count,
+                      int latents_per_workgroup, int keys_per_tile) {
+    if (latents_per_workgroup < 1 || keys_per_tile < 1 || cu_count < 1) return 1;
+    return plan_splits(batch_size, N_latent, N_input, cu_count, latents_per_workgroup,
+                       keys_per_tile);
+}
+
 void launch_naive_kernel(const float* Q, const float* K, const float* V, float* output,
                          int batch_size, int N_latent, int N_input, int dim, hipStream_t stream) {
     const char* who = "launch_naive_kernel";

@@ -271,17 +271,21 @@ void flash_f32_kernel(Params p) {
     }
 }
 
-// Log-sum-exp merge of split partials (kernel_splitk.cu:186-236), one
-// wavefront per (batch, latent) row, 3 float4 of the 768-wide row per lane.
-__global__ __launch_bounds__(256)
+// Log-sum-exp merge of split partials (kernel_splitk.cu:186-236).  One
+// workgroup of 192 threads per (batch, latent) row: each wave first reduces
+// M = max pm and L = sum exp(pm - M) pl over the splits (lane-strided), then
+// thread c accumulates float4 column c over the splits with 8 partial rows in
+// flight at a time.  HBM-bound: reads S * 3 KiB of po per row.
+constexpr int kCombineThreads = kDim / 4;  // 192
+
+__global__ __launch_bounds__(kCombineThreads)
 void lse_combine_kernel(const float* __restrict__ po, const float* __restrict__ pm,
-                        const float* __restrict__ pl, float* __restrict__ out,
-                        int rows, int S) {
-    const int row = blockIdx.x * 4 + (threadIdx.x >> 6);
-    if (row >= rows) return;
+                        const float* __restrict__ pl, float* __restrict__ out, int S) {
+    const size_t row = blockIdx.x;
     const int lane = threadIdx.x & 63;
-    const float* pmr = pm + (size_t)row * S;
-    const float* plr = pl + (size_t)row * S;
+    const int c = threadIdx.x;
+    const float* pmr = pm + row * S;
+    const float* plr = pl + row * S;
 
     float M = -FLT_MAX;
     for (int s = lane; s < S; s += kWave) M = fmaxf(M, pmr[s]);
@@ -293,21 +297,27 @@ void lse_combine_kernel(const float* __restrict__ po, const float* __restrict__ 
     }
     L = wave_sum(L);
 
-    f4 a0 = {0.f, 0.f, 0.f, 0.f}, a1 = a0, a2 = a0;
-    for (int s = 0; s < S; ++s) {
+    const f4* src = (const f4*)(po + row * S * kDim) + c;
+    f4 acc = {0.f, 0.f, 0.f, 0.f};
+    int s = 0;
+    for (; s + 8 <= S; s += 8) {
+        f4 v[8];
+        float wgt[8];
+#pragma unroll
+        for (int u = 0; u < 8; ++u) {
+            v[u] = src[(size_t)(s + u) * (kDim / 4)];
+            const float m = pmr[s + u];
+            wgt[u] = (m == -FLT_MAX) ? 0.f : expf(m - M);
+        }
+#pragma unroll
+        for (int u = 0; u < 8; ++u) acc += wgt[u] * v[u];
+    }
+    for (; s < S; ++s) {
         const float m = pmr[s];
         if (m == -FLT_MAX) continue;
-        const float wgt = expf(m - M);
-        const f4* src = (const f4*)(po + ((size_t)row * S + s) * kDim);
-        a0 += wgt * src[lane];
-        a1 += wgt * src[lane + 64];
-        a2 += wgt * src[lane + 128];
+        acc += expf(m - M) * src[(size_t)s * (kDim / 4)];
     }
-    const float inv = 1.0f / (L + 1e-6f);
-    f4* dst = (f4*)(out + (size_t)row * kDim);
-    dst[lane] = a0 * inv;
-    dst[lane + 64] = a1 * inv;
-    dst[lane + 128] = a2 * inv;
+    ((f4*)(out + row * kDim))[c] = acc * (1.0f / (L + 1e-6f));
 }
 
 }  // namespace f32
@@ -343,8 +353,8 @@ bool launch_flash_f32(const float* Q, const float* K, const float* V, float* out
 bool launch_lse_combine(const float* po, const float* pm, const float* pl, float* out,
                         int rows, int S, hipStream_t stream) {
     if (rows <= 0) return true;
-    hipLaunchKernelGGL(f32::lse_combine_kernel, dim3((rows + 3) / 4), dim3(256), 0, stream,
-                       po, pm, pl, out, rows, S);
+    hipLaunchKernelGGL(f32::lse_combine_kernel, dim3(rows), dim3(f32::kCombineThreads), 0,
+                       stream, po, pm, pl, out, S);
     return check_launch("lse_combine");
 }
 

@@ -140,6 +140,24 @@ lib.xattn_xcd_remap.argtypes = [_I, _I]
 lib.xattn_xcd_remap.restype = ctypes.c_int
 lib.xattn_optimized_num_splits.argtypes = [_I, _I, _I, _I]
 lib.xattn_optimized_num_splits.restype = ctypes.c_int
+lib.xattn_plan_splits.argtypes = [_I, _I, _I, _I, _I, _I]
+lib.xattn_plan_splits.restype = ctypes.c_int
+
+# Workgroup shape of the MFMA kernels (csrc/xattn_flash_*.hip): 64 latents per
+# workgroup; 16-key tiles (fp32) and 32-key tiles (fp16/bf16).
+LATENTS_PER_WORKGROUP = 64
+KEYS_PER_TILE_F32 = 16
+KEYS_PER_TILE_F16 = 32
+
+
+def plan_num_splits(N_latent, N_input, batch_size, sm_count, keys_per_tile=KEYS_PER_TILE_F32):
+    """Default num_splits of the split-K drivers: enough key splits for the
+    64-latent workgroups to fill ``sm_count`` compute units once, each split a
+    whole number of tiles.  (The reference's ``choose_num_splits`` sizes for
+    4-latent blocks and 4x oversubscription; it is kept unchanged for callers
+    that use it directly.)"""
+    return max(1, lib.xattn_plan_splits(batch_size, N_latent, N_input, int(sm_count),
+                                        LATENTS_PER_WORKGROUP, keys_per_tile))
 
 
 def _bind_optional(name, argtypes):
@@ -552,7 +570,7 @@ def benchmark_splitk_events(Q, K, V, batch_size, N_latent, N_input, D,
                            "with csrc/xattn_flash_f32.hip).")
     _require_dim(D, "split-K")
     if num_splits is None:
-        num_splits = choose_num_splits(N_latent, N_input, batch_size, sm_count)
+        num_splits = plan_num_splits(N_latent, N_input, batch_size, sm_count)
     Q = _prep(Q, batch_size)
     K = _prep(K, batch_size)
     V = _prep(V, batch_size)
@@ -661,8 +679,8 @@ def _wmma_splitk(launch_fn, what, Q, K, V, batch_size, N_latent, N_input, D, war
                  num_splits, sm_count, bf16, keep_partials=False):
     _require_dim(D, what)
     if num_splits is None:
-        num_splits = choose_num_splits(N_latent, N_input, batch_size, sm_count,
-                                       latents_per_block=16)
+        num_splits = plan_num_splits(N_latent, N_input, batch_size, sm_count,
+                                     KEYS_PER_TILE_F16)
     Qh, Kh, Vh = _half_inputs(Q, K, V, batch_size, D, bf16)
     launch = lambda q, k, v, *rest: launch_fn(q, k, v, *rest)  # noqa: E731
     res = _splitk_run(launch, Qh, Kh, Vh, batch_size, N_latent, N_input, D, num_splits,

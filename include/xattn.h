@@ -39,13 +39,14 @@ void launch_naive_kernel(const float* Q, const float* K, const float* V,
 
 /* Replaces launch_parallel_kernel, kernel_warp_parallel.cu:113-123.
  * One 64-lane wavefront per latent; the full score row lives in LDS,
- * (4 * N_input + 4) * 4 bytes per workgroup.  dim <= 768, dim % 4 == 0. */
+ * (4 * N_input + 4) * 4 bytes per workgroup (refused when that exceeds the
+ * device's per-workgroup LDS).  1 <= dim <= 768. */
 void launch_parallel_kernel(const float* Q, const float* K, const float* V,
                             float* output, int batch_size, int N_latent,
                             int N_input, int dim, hipStream_t stream);
 
 /* Replaces launch_tiled_kernel, kernel_tiled.cu:169-179.
- * 16-key K tiles staged in LDS, online softmax.  dim <= 768, dim % 4 == 0. */
+ * 16-key K tiles staged in LDS, online softmax.  1 <= dim <= 768. */
 void launch_tiled_kernel(const float* Q, const float* K, const float* V,
                          float* output, int batch_size, int N_latent,
                          int N_input, int dim, hipStream_t stream);
@@ -133,6 +134,13 @@ int xattn_xcd_remap(int block, int num_blocks);
 /* Number of key splits launch_optimized_kernel uses internally. */
 int xattn_optimized_num_splits(int batch_size, int N_latent, int N_input,
                                int cu_count);
+/* Key splits that make batch_size * ceil(N_latent / latents_per_workgroup)
+ * workgroups fill cu_count compute units once, each split a whole number of
+ * keys_per_tile-key tiles.  Both MFMA kernels use 64 latents per workgroup;
+ * tiles are 16 keys (fp32) and 32 keys (fp16/bf16).  Replaces the
+ * block-count heuristic of cuda_wrappers.py:456-467 for these kernels. */
+int xattn_plan_splits(int batch_size, int N_latent, int N_input, int cu_count,
+                      int latents_per_workgroup, int keys_per_tile);
 
 #ifdef __cplusplus
 }
