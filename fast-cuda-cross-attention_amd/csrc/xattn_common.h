@@ -41,17 +41,28 @@ __host__ __device__ inline int xcd_remap(int bid, int n) {
 // --------------------------------------------------------------------------
 // Wave-level helpers
 // --------------------------------------------------------------------------
-__device__ inline float wave_max16_groups(float v) {
-    // max over the 4 lanes {l, l^16, l^32, l^48}
-    v = fmaxf(v, __shfl_xor(v, 16));
-    v = fmaxf(v, __shfl_xor(v, 32));
-    return v;
+// Reductions over the 4 lanes {l, l^16, l^32, l^48} with the gfx950 row
+// swaps (v_permlane16_swap / v_permlane32_swap): each returns the pair
+// (own value, value of the partner row), so no LDS round trip is involved.
+__device__ inline float xor16_partner_max(float v) {
+    const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v),
+                                                    false, false);
+    return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
 }
-
+__device__ inline float xor32_partner_max(float v) {
+    const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v),
+                                                    false, false);
+    return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+__device__ inline float wave_max16_groups(float v) {
+    return xor32_partner_max(xor16_partner_max(v));
+}
 __device__ inline float wave_sum16_groups(float v) {
-    v += __shfl_xor(v, 16);
-    v += __shfl_xor(v, 32);
-    return v;
+    auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false,
+                                              false);
+    v = __uint_as_float(r[0]) + __uint_as_float(r[1]);
+    r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    return __uint_as_float(r[0]) + __uint_as_float(r[1]);
 }
 
 __device__ inline float wave_sum(float v) {
@@ -94,6 +105,17 @@ __device__ inline void lds_barrier() {
     __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0), vmcnt/expcnt unconstrained
     __builtin_amdgcn_s_barrier();
     compiler_fence();
+}
+
+// A wave-uniform pointer re-materialised through readfirstlane: the compiler
+// cannot re-associate (uniform base + per-lane offset) across it and hoist
+// per-lane 64-bit sums out of a loop, and the base lands in SGPRs.
+template <typename T>
+__device__ inline const T* uniform_ptr(const T* p) {
+    const unsigned long long v = (unsigned long long)p;
+    const unsigned lo = __builtin_amdgcn_readfirstlane((unsigned)v);
+    const unsigned hi = __builtin_amdgcn_readfirstlane((unsigned)(v >> 32));
+    return (const T*)(((unsigned long long)hi << 32) | lo);
 }
 
 // 16-byte global -> LDS DMA for one lane.  The 64 lanes of the wave land at

@@ -5,23 +5,30 @@
 // score is the plain dot product q.k.
 //
 // Work item = (batch, key split, 64 latents); 4 wavefronts x 16 latents, the
-// same S^T formulation as the fp32 kernel:
+// S^T formulation of the fp32 kernel with 32-key tiles:
 //
 //   S^T[32 keys x 16 q] = K_tile . Q^T       2 x 24 MFMA (k = 32)
 //   O[16 q x 768]     += P[16 q x 32 keys] . V_tile     48 MFMA (k = 32)
 //
-// After the two S^T MFMAs (keys 0..15 and 16..31 of the tile), lane (j, g)
-// holds S[q = j][4g + i] and S[q = j][16 + 4g + i], i < 4: eight scores, which
-// become the eight k-values of its P operand directly.  The matching V operand
-// needs those eight keys contiguous for one d, so V is written into LDS
-// transposed, Vt[d][pos] with pos = 8g + e for key 4g + e (e < 4) and
-// 16 + 4g + (e - 4) (e >= 4): one 16-byte read per lane per MFMA.
+// After the two S^T MFMAs (tile keys 0..15 and 16..31), lane (j, g) holds
+// S[q = j][4g + i] and S[q = j][16 + 4g + i], i < 4: the eight k-values of its
+// P operand.  The V operand needs, in lane (j, g), V[4g + e][d0 + j] and
+// V[16 + 4g + e][d0 + j]: eight keys of one column.  gfx950's transposing LDS
+// read (ds_read_b64_tr_b16) delivers exactly that from a row-major V tile:
+// within each 16-lane group, lane i receives element (i mod 4) of the 8-byte
+// rows read by lanes 4e + i/4 (e < 4), so lane 4e + q of group g points at
+// V[4g + e][d0 + 4q] and lane j gets V[4g + e][d0 + j] for e = 0..3.
 //
-// K tile (32 x 768, 48 KiB) arrives by global->LDS DMA into a row-major layout
-// whose 16-byte blocks are XOR-swizzled by (row & 15), which keeps the 16 rows
-// read by one MFMA on distinct banks without padding (padding would break the
-// 1 KiB DMA chunks).  K is double-buffered; V goes global -> VGPR -> transpose
-// -> LDS one tile ahead.  LDS: 2 x 48 KiB (K) + 60 KiB (Vt) = 156 KiB.
+// K and V therefore both arrive by global->LDS DMA into row-major tiles, one
+// pipeline for both (as in the fp32 kernel): phases alternate QK(t) / PV(t),
+// phase p reads buffer p % 3 and requests phase p + 2.  Tiles are 32 x 768
+// (48 KiB); 3 buffers = 144 KiB.  The 16-byte blocks of row r are XOR-swizzled
+// by f(r) = 2(r & 7) + ((r >> 3) & 1), which is distinct for 16 consecutive
+// rows (the 16 rows of one b128 K read hit 16 different 4-bank groups) and
+// keeps the 32-byte column pairs of 8 consecutive rows apart (one transposed V
+// read of 32 lanes covers all 64 banks once), so neither reader conflicts and
+// no padding breaks the contiguous 1 KiB DMA chunks.  K and V tiles share the
+// layout, hence the per-lane DMA offsets.
 #include "xattn_common.h"
 
 namespace xattn {
@@ -31,18 +38,16 @@ constexpr int BN = 32;                 // keys per tile
 constexpr int QW = 16;                 // latents per wavefront
 constexpr int NW = 4;
 constexpr int BM = QW * NW;            // 64 latents per workgroup
-constexpr int KBLK = kDim / 8;         // 16-byte blocks per K row (96)
-constexpr int KBUF = BN * kDim;        // halves per K buffer
-constexpr int VT_ROW = BN + 8;         // Vt row stride in halves (80 B: conflict-free reads)
-constexpr int VT_BUF = kDim * VT_ROW;  // halves
-constexpr int K_CHUNKS = BN * KBLK / kWave;  // 1 KiB DMA chunks per K tile (48)
-constexpr int K_CPW = K_CHUNKS / NW;         // per wavefront (12)
-constexpr int V_UNITS = (BN / 4) * KBLK;     // 4 keys x 8 d units per tile (768)
-constexpr int V_UPT = V_UNITS / (NW * kWave);  // per thread (3)
-constexpr float kTauLog2 = 8.0f;
+constexpr int KBLK = kDim / 8;         // 16-byte blocks per row (96)
+constexpr int BUF = BN * kDim;         // halves per tile buffer
+constexpr int NBUF = 3;
+constexpr int CHUNKS = BN * KBLK / kWave;  // 1 KiB DMA chunks per tile (48)
+constexpr int CPW = CHUNKS / NW;           // per wavefront (12)
+// A row's weights are exp2(s - m_ref) with m_ref fixed for a whole pass over
+// the keys; a pass restarts when some score exceeds m_ref by 2^kTauLog2.
+constexpr float kTauLog2 = 64.0f;
 
-static_assert((2 * KBUF + VT_BUF) * 2 <= 160 * 1024, "LDS budget");
-static_assert(V_UNITS % (NW * kWave) == 0, "V units per thread");
+static_assert(NBUF * BUF * 2 <= 160 * 1024, "LDS budget");
 
 struct Params {
     const u16* Q;
@@ -56,6 +61,8 @@ struct Params {
 };
 
 typedef unsigned int u4v __attribute__((ext_vector_type(4)));
+typedef short s4 __attribute__((ext_vector_type(4)));
+typedef short s8v __attribute__((ext_vector_type(8)));
 
 // Operand vector type of the MFMA for element type T (8 x 16-bit).
 template <typename T> struct Vec8;
@@ -76,15 +83,19 @@ __device__ inline unsigned pack2(float lo, float hi) {
     return (unsigned)__builtin_bit_cast(u16, a) | ((unsigned)__builtin_bit_cast(u16, b) << 16);
 }
 
-// Swizzled position (in 16-byte blocks) of block c of K-tile row r.
-__device__ inline int kpos(int r, int c) { return r * KBLK + (c ^ (r & 15)); }
+// swizzle of the 16-byte blocks of tile row r
+__device__ inline int swz(int r) { return 2 * (r & 7) + ((r >> 3) & 1); }
+
+__device__ inline s4 tr_read(const u16* p) {
+    return __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+        (__attribute__((address_space(3))) s4*)(p));
+}
 
 template <typename T, bool PARTIAL>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1)))
 void flash16_kernel(Params p) {
     typedef typename Vec8<T>::type v8;
-    __shared__ __attribute__((aligned(16))) u16 lds[2 * KBUF + VT_BUF];
-    u16* const vt = lds + 2 * KBUF;
+    __shared__ __attribute__((aligned(16))) u16 lds[NBUF * BUF];
 
     const int item = xcd_remap(blockIdx.x, gridDim.x);
     const int rb = item % p.row_blocks;
@@ -125,61 +136,36 @@ void flash16_kernel(Params p) {
     const u16* Kb = p.K + (size_t)b * p.NI * kDim;
     const u16* Vb = p.V + (size_t)b * p.NI * kDim;
     const int ntiles = (k1 - k0 + BN - 1) / BN;
+    const int nphase = 2 * ntiles;
 
-    // K tile -> LDS by DMA: chunk m of the tile fills swizzled blocks
-    // [64m, 64m + 64); lane i fetches the global block that belongs at 64m + i.
-    auto issue_k = [&](int tile) {
-        u16* buf = lds + (tile & 1) * KBUF;
-        const int n0 = k0 + tile * BN;
+    // DMA: chunk m of a tile fills swizzled blocks [64m, 64m + 64); lane i
+    // fetches the global block that belongs at 64m + i.  For a full tile the
+    // per-lane element offset of chunk w*CPW + t is dofs[t].
+    unsigned dofs[CPW];
 #pragma unroll
-        for (int t = 0; t < K_CPW; ++t) {
-            const int m = w * K_CPW + t;
-            const int P = 64 * m + lane;
-            const int r = P / KBLK;
-            const int c = (P - r * KBLK) ^ (r & 15);
-            const int key = min(n0 + r, k1 - 1);
-            dma16(Kb + (size_t)key * kDim + 8 * c, buf + 64 * 8 * m);
-        }
-    };
-
-    // V tile -> registers: unit u = tid + 256 x covers keys 4kg..4kg+3 and
-    // d = 8db..8db+7 with kg = u % 8, db = u / 8: per load, 8 lanes read 128
-    // contiguous bytes of one row, and the transposed 8-byte writes of one
-    // instruction fall on 32 distinct banks (4-way instead of 32-way).
-    u4v vreg[V_UPT][4];
-    auto load_v = [&](int tile) {
-        const int n0 = k0 + tile * BN;
+    for (int t = 0; t < CPW; ++t) {
+        const int P = 64 * (w * CPW + t) + lane;
+        const int r = P / KBLK;
+        dofs[t] = (unsigned)(r * kDim + 8 * ((P - r * KBLK) ^ swz(r)));
+    }
+    auto issue = [&](int ph) {
+        const int n0 = k0 + (ph >> 1) * BN;
+        const u16* src = uniform_ptr(((ph & 1) ? Vb : Kb) + (size_t)n0 * kDim);
+        u16* buf = lds + (ph % NBUF) * BUF;
+        const int last = k1 - 1 - n0;  // last valid row of this tile
+        if (last >= BN - 1) {
 #pragma unroll
-        for (int x = 0; x < V_UPT; ++x) {
-            const int u = tid + 256 * x;
-            const int kg = u & 7, db = u >> 3;
+            for (int t = 0; t < CPW; ++t) dma16(src + dofs[t], buf + 64 * 8 * (w * CPW + t));
+        } else {
+            // partial tile: rows past k1 re-read the last valid row (their
+            // scores are masked to -inf and their weights are 0)
 #pragma unroll
-            for (int e = 0; e < 4; ++e) {
-                const int key = min(n0 + 4 * kg + e, k1 - 1);
-                vreg[x][e] = *(const u4v*)(Vb + (size_t)key * kDim + 8 * db);
-            }
-        }
-    };
-    // registers -> Vt[d][pos(key)], 4 keys (8 bytes) per write
-    auto store_vt = [&]() {
-#pragma unroll
-        for (int x = 0; x < V_UPT; ++x) {
-            const int u = tid + 256 * x;
-            const int kg = u & 7, db = u >> 3;
-            const int pos = kg < 4 ? 8 * kg : 8 * (kg - 4) + 4;
-#pragma unroll
-            for (int h = 0; h < 4; ++h) {  // column pair (2h, 2h+1) of the 8 columns
-                const unsigned r0 = vreg[x][0][h], r1 = vreg[x][1][h];
-                const unsigned r2 = vreg[x][2][h], r3 = vreg[x][3][h];
-                // low halves -> column 2h, high halves -> column 2h+1
-                const unsigned lo01 = __builtin_amdgcn_perm(r1, r0, 0x05040100u);
-                const unsigned lo23 = __builtin_amdgcn_perm(r3, r2, 0x05040100u);
-                const unsigned hi01 = __builtin_amdgcn_perm(r1, r0, 0x07060302u);
-                const unsigned hi23 = __builtin_amdgcn_perm(r3, r2, 0x07060302u);
-                const int d = 8 * db + 2 * h;
-                typedef unsigned u2v __attribute__((ext_vector_type(2)));
-                *(u2v*)(vt + (size_t)d * VT_ROW + pos) = (u2v){lo01, lo23};
-                *(u2v*)(vt + (size_t)(d + 1) * VT_ROW + pos) = (u2v){hi01, hi23};
+            for (int t = 0; t < CPW; ++t) {
+                const int P = 64 * (w * CPW + t) + lane;
+                const int r = P / KBLK;
+                const int c = (P - r * KBLK) ^ swz(r);
+                dma16(src + (unsigned)(min(r, last) * kDim + 8 * c),
+                      buf + 64 * 8 * (w * CPW + t));
             }
         }
     };
@@ -192,100 +178,145 @@ void flash16_kernel(Params p) {
 #pragma unroll
         for (int s = 0; s < 24; ++s) qr[s] = *(const v8*)(qrow + 32 * s);
     }
-    issue_k(0);
-    load_v(0);
 
-    f4 acc[48];
+    // LDS read bases (in halves, relative to a tile buffer).  f(r) < 16, so
+    // the swizzle only touches the low 4 bits of a block index.
+    // K (QK, A operand): row j, block 4s + g, s = 4a + bb ->
+    //   j*768 + 128a + 8((4bb + g) ^ f(j)); rows 16 + j (f(16 + j) = f(j)) are
+    //   16*768 further.
+    int kofs[4];
 #pragma unroll
-    for (int t = 0; t < 48; ++t) acc[t] = (f4){0.f, 0.f, 0.f, 0.f};
-
-    const float tau_raw = kTauLog2 / kLog2e;
-    float m_true = -FLT_MAX, m_used = -FLT_MAX, lsum = 0.f;
-
-    for (int tile = 0; tile < ntiles; ++tile) {
-        const int n0 = k0 + tile * BN;
-        wait_vmcnt<V_UPT * 4>();  // K(tile) landed; V(tile) loads may be in flight
-        lds_barrier();            // and every wave is done with Vt and K(tile-1)
-        if (tile + 1 < ntiles) issue_k(tile + 1);
-        store_vt();
-        if (tile + 1 < ntiles) load_v(tile + 1);
-
-        // ---------------- QK: two 16-key halves ----------------
-        f4 sa = {0.f, 0.f, 0.f, 0.f}, sb = sa;
-        {
-            const u16* kb = lds + (tile & 1) * KBUF;
-            v8 ka[3], kbv[3];
-            ka[0] = *(const v8*)(kb + 8 * kpos(j, g));
-            kbv[0] = *(const v8*)(kb + 8 * kpos(16 + j, g));
-            ka[1] = *(const v8*)(kb + 8 * kpos(j, 4 + g));
-            kbv[1] = *(const v8*)(kb + 8 * kpos(16 + j, 4 + g));
+    for (int bb = 0; bb < 4; ++bb) kofs[bb] = j * kDim + 8 * ((4 * bb + g) ^ swz(j));
+    // V (PV, transposed read): lane 4e + q of group g reads row 4g + e at
+    // column 16t + 4q, i.e. block 2t + (q >> 1) at byte 8 (q & 1) ->
+    //   row*768 + 128(t >> 3) + 8((2(t & 7) + (q >> 1)) ^ f(row)) + 4(q & 1).
+    int vofs[8];
+    {
+        const int e = j >> 2, q = j & 3;
+        const int row = 4 * g + e;
 #pragma unroll
-            for (int s = 0; s < 24; ++s) {
-                if (s + 2 < 24) {
-                    ka[(s + 2) % 3] = *(const v8*)(kb + 8 * kpos(j, 4 * (s + 2) + g));
-                    kbv[(s + 2) % 3] = *(const v8*)(kb + 8 * kpos(16 + j, 4 * (s + 2) + g));
-                }
-                sa = mfma32<T>(ka[s % 3], qr[s], sa);
-                sb = mfma32<T>(kbv[s % 3], qr[s], sb);
-                __builtin_amdgcn_sched_barrier(0);
-            }
-        }
-
-        // ---------------- online softmax (raw-dot units) ----------------
-        float x[8];
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            x[i] = (n0 + 4 * g + i < k1) ? sa[i] : -INFINITY;
-            x[4 + i] = (n0 + 16 + 4 * g + i < k1) ? sb[i] : -INFINITY;
-        }
-        float tmax = x[0];
-#pragma unroll
-        for (int i = 1; i < 8; ++i) tmax = fmaxf(tmax, x[i]);
-        tmax = wave_max16_groups(tmax);
-        m_true = fmaxf(m_true, tmax);
-        const bool grow = tmax > m_used + tau_raw;
-        if (__any(grow)) {
-            const float m_new = grow ? tmax : m_used;
-            const float alpha = fast_exp2((m_used - m_new) * kLog2e);
-            lsum *= alpha;
-            m_used = m_new;
-            float a[4];
-#pragma unroll
-            for (int i = 0; i < 4; ++i) a[i] = __shfl(alpha, 4 * g + i);
-#pragma unroll
-            for (int t = 0; t < 48; ++t)
-#pragma unroll
-                for (int i = 0; i < 4; ++i) acc[t][i] *= a[i];
-        }
-        float pw[8];
-        float rs = 0.f;
-#pragma unroll
-        for (int i = 0; i < 8; ++i) {
-            pw[i] = fast_exp2((x[i] - m_used) * kLog2e);
-            rs += pw[i];
-        }
-        lsum += wave_sum16_groups(rs);
-        const v8 pa = __builtin_bit_cast(
-            v8, ((u4v){pack2<T>(pw[0], pw[1]), pack2<T>(pw[2], pw[3]), pack2<T>(pw[4], pw[5]),
-                       pack2<T>(pw[6], pw[7])}));
-
-        // ---------------- PV ----------------
-        lds_barrier();  // Vt of this tile written by every wave
-        {
-            const u16* vb = vt + (size_t)j * VT_ROW + 8 * g;
-            v8 vv[3];
-            vv[0] = *(const v8*)(vb);
-            vv[1] = *(const v8*)(vb + 16 * VT_ROW);
-#pragma unroll
-            for (int t = 0; t < 48; ++t) {
-                if (t + 2 < 48) vv[(t + 2) % 3] = *(const v8*)(vb + (size_t)16 * (t + 2) * VT_ROW);
-                acc[t] = mfma32<T>(pa, vv[t % 3], acc[t]);
-                __builtin_amdgcn_sched_barrier(0);
-            }
-        }
+        for (int t8 = 0; t8 < 8; ++t8)
+            vofs[t8] = row * kDim + 8 * ((2 * t8 + (q >> 1)) ^ swz(row)) + 4 * (q & 1);
     }
 
-    const float factor = fast_exp2((m_used - m_true) * kLog2e);
+    __shared__ int restart_flag;
+    if (tid == 0) restart_flag = 0;
+
+    const float tau_raw = kTauLog2 / kLog2e;
+    // m_true: exact running max of this lane's latent; m_ref: the reference
+    // of the weights, fixed for a pass (set on the first tile of the first
+    // pass, raised to m_true when a pass restarts).
+    float m_true = -FLT_MAX, m_ref = -FLT_MAX, lsum;
+    f4 acc[48];
+
+    for (;;) {  // passes over the key range; the second one is rare
+        issue(0);
+        issue(1);
+#pragma unroll
+        for (int t = 0; t < 48; ++t) acc[t] = (f4){0.f, 0.f, 0.f, 0.f};
+        lsum = 0.f;
+        bool restart = false;
+
+        for (int tile = 0; tile < ntiles; ++tile) {
+            const int n0 = k0 + tile * BN;
+            int ph = 2 * tile;
+
+            // ---------------- QK phase ----------------
+            wait_vmcnt<CPW>();
+            lds_barrier();
+            if (ph + 2 < nphase) issue(ph + 2);
+            f4 sa = {0.f, 0.f, 0.f, 0.f}, sb = sa;
+            {
+                const u16* kb = lds + (ph % NBUF) * BUF;
+                v8 ka[3], kv[3];
+                ka[0] = *(const v8*)(kb + kofs[0]);
+                kv[0] = *(const v8*)(kb + kofs[0] + 16 * kDim);
+                ka[1] = *(const v8*)(kb + kofs[1]);
+                kv[1] = *(const v8*)(kb + kofs[1] + 16 * kDim);
+#pragma unroll
+                for (int s = 0; s < 24; ++s) {
+                    if (s + 2 < 24) {
+                        const int sn = s + 2;
+                        const u16* pk = kb + kofs[sn & 3] + 128 * (sn >> 2);
+                        ka[sn % 3] = *(const v8*)(pk);
+                        kv[sn % 3] = *(const v8*)(pk + 16 * kDim);
+                    }
+                    sa = mfma32<T>(ka[s % 3], qr[s], sa);
+                    sb = mfma32<T>(kv[s % 3], qr[s], sb);
+                    __builtin_amdgcn_sched_barrier(0);
+                }
+            }
+
+            // ---------------- softmax weights (raw-dot units) ----------------
+            float x[8];
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                x[i] = (n0 + 4 * g + i < k1) ? sa[i] : -INFINITY;
+                x[4 + i] = (n0 + 16 + 4 * g + i < k1) ? sb[i] : -INFINITY;
+            }
+            float tmax = x[0];
+#pragma unroll
+            for (int i = 1; i < 8; ++i) tmax = fmaxf(tmax, x[i]);
+            tmax = wave_max16_groups(tmax);
+            m_true = fmaxf(m_true, tmax);
+            if (m_ref == -FLT_MAX) m_ref = tmax;
+            if (__any(tmax > m_ref + tau_raw) && lane == 0) restart_flag = 1;
+            float pw[8];
+            float rs = 0.f;
+#pragma unroll
+            for (int i = 0; i < 8; ++i) {
+                pw[i] = fast_exp2((x[i] - m_ref) * kLog2e);
+                rs += pw[i];
+            }
+            lsum += wave_sum16_groups(rs);
+            const v8 pa = __builtin_bit_cast(
+                v8, ((u4v){pack2<T>(pw[0], pw[1]), pack2<T>(pw[2], pw[3]),
+                           pack2<T>(pw[4], pw[5]), pack2<T>(pw[6], pw[7])}));
+
+            // ---------------- PV phase ----------------
+            ph += 1;
+            if (ph + 1 < nphase) wait_vmcnt<CPW>();
+            else wait_vmcnt<0>();
+            lds_barrier();
+            if (__builtin_amdgcn_readfirstlane(restart_flag)) {  // uniform over the workgroup
+                restart = true;
+                break;
+            }
+            if (ph + 2 < nphase) issue(ph + 2);
+            {
+                const u16* vb = lds + (ph % NBUF) * BUF;
+                s4 va[3], vc[3];
+                va[0] = tr_read(vb + vofs[0]);
+                vc[0] = tr_read(vb + vofs[0] + 16 * kDim);
+                va[1] = tr_read(vb + vofs[1]);
+                vc[1] = tr_read(vb + vofs[1] + 16 * kDim);
+#pragma unroll
+                for (int t = 0; t < 48; ++t) {
+                    if (t + 2 < 48) {
+                        const int tn = t + 2;
+                        const u16* pv = vb + vofs[tn & 7] + 128 * (tn >> 3);
+                        va[tn % 3] = tr_read(pv);
+                        vc[tn % 3] = tr_read(pv + 16 * kDim);
+                    }
+                    const s8v both = __builtin_shufflevector(va[t % 3], vc[t % 3], 0, 1, 2, 3,
+                                                             4, 5, 6, 7);
+                    acc[t] = mfma32<T>(pa, __builtin_bit_cast(v8, both), acc[t]);
+                    __builtin_amdgcn_sched_barrier(0);
+                }
+            }
+        }
+        if (!restart) break;
+        // Some latent's scores outgrew its reference: drain the DMA, clear the
+        // flag, and run the keys again with the reference raised to the max
+        // seen so far.
+        wait_vmcnt<0>();
+        lds_barrier();
+        if (tid == 0) restart_flag = 0;
+        m_ref = m_true;
+        lds_barrier();
+    }
+
+    const float factor = fast_exp2((m_ref - m_true) * kLog2e);
     const float rowscale = PARTIAL ? factor : factor / (lsum * factor + 1e-6f);
     float rsc[4];
 #pragma unroll

@@ -95,3 +95,24 @@ def test_splitk_long_input(cw, oracle, bf16):
     out, _, _, s = fn(q, k, v, 1, 256, 16384, 768, warmup=1, iters=1, sm_count=cu)
     assert s > 1
     _check(oracle, cw, out, q, k, v, bf16)
+
+
+@pytest.mark.parametrize("bf16", [False, True], ids=["fp16", "bf16"])
+def test_growing_scores_force_restarts(cw, oracle, bf16):
+    """Scores rise by ~0.43 per key (~124 in exp2 units over the row), far past
+    the reference the weights are taken against, so every row restarts its
+    pass over the keys at least once."""
+    rng = np.random.RandomState(8)
+    nl, ni = 40, 200
+    u = rng.randn(768)
+    u /= np.linalg.norm(u)
+    q = (u * np.sqrt(768.0) * (1.0 + 0.01 * rng.randn(nl, 1))
+         + 0.1 * rng.randn(nl, 768))[None].astype(np.float32)
+    k = (np.arange(ni)[:, None] * (12.0 / np.sqrt(768.0)) * u
+         + 0.05 * rng.randn(ni, 768))[None].astype(np.float32)
+    v = rng.randn(1, ni, 768).astype(np.float32)
+    for perm in (rng.permutation(ni), np.arange(ni)):
+        kp, vp = k[:, perm], v[:, perm]
+        out = _run(cw, q, kp, vp, bf16)
+        tight = oracle.rel_err(out, _rounded_ref(oracle, cw, q, kp, vp, bf16))
+        assert np.all(np.isfinite(out)) and tight <= 2 * TIGHT[bf16], tight
