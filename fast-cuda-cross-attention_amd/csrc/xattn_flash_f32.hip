@@ -121,13 +121,28 @@ void flash_f32_kernel(Params p) {
         const float* src = (ph & 1) ? Vb : Kb;
         float* buf = lds + (ph % NBUF) * BUF;
         const int n0 = k0 + (ph >> 1) * BN;
+        // this wave's chunks cover tile rows r0 .. r0 + CPW/3 - 1, 3 chunks each
+        const int r0 = w * (CPW / ROW_CHUNKS);
+        if (n0 + BN <= k1) {
+            // full tile: one wave-uniform base, compile-time chunk offsets,
+            // lane * 16 B the only per-lane part
+            const float* base = uniform_ptr(src + (size_t)(n0 + r0) * kDim);
 #pragma unroll
-        for (int t = 0; t < CPW; ++t) {
-            const int ch = w * CPW + t;
-            const int r = ch / ROW_CHUNKS, c = ch % ROW_CHUNKS;
-            const int key = min(n0 + r, k1 - 1);
-            dma16(src + (size_t)key * kDim + c * (kWave * 4) + lane * 4,
-                  buf + r * ROW + c * (kWave * 4));
+            for (int t = 0; t < CPW; ++t) {
+                const int r = t / ROW_CHUNKS, c = t % ROW_CHUNKS;
+                dma16(base + r * kDim + c * (kWave * 4) + lane * 4,
+                      buf + (r0 + r) * ROW + c * (kWave * 4));
+            }
+        } else {
+            // last, partial tile: rows past k1 re-read row k1-1 (their scores
+            // are masked to -inf and their weights are 0)
+#pragma unroll
+            for (int t = 0; t < CPW; ++t) {
+                const int r = t / ROW_CHUNKS, c = t % ROW_CHUNKS;
+                const int key = min(n0 + r0 + r, k1 - 1);
+                dma16(uniform_ptr(src + (size_t)key * kDim + c * (kWave * 4)) + lane * 4,
+                      buf + (r0 + r) * ROW + c * (kWave * 4));
+            }
         }
     };
 
