@@ -44,8 +44,11 @@ constexpr int NBUF = 3;
 constexpr int CHUNKS = BN * KBLK / kWave;  // 1 KiB DMA chunks per tile (48)
 constexpr int CPW = CHUNKS / NW;           // per wavefront (12)
 // A row's weights are exp2(s - m_ref) with m_ref fixed for a whole pass over
-// the keys; a pass restarts when some score exceeds m_ref by 2^kTauLog2.
-constexpr float kTauLog2 = 64.0f;
+// the keys; a pass restarts when some score exceeds m_ref by tau_log2<T> (in
+// exp2 units), which bounds every weight by 2^tau_log2<T> in the MFMA's input
+// type: 2^15 for fp16 (largest finite 65504), 2^64 for bf16 (fp32's range).
+template <typename T> constexpr float tau_log2 = 64.0f;
+template <> constexpr float tau_log2<_Float16> = 15.0f;
 
 static_assert(NBUF * BUF * 2 <= 160 * 1024, "LDS budget");
 
@@ -202,7 +205,7 @@ void flash16_kernel(Params p) {
     __shared__ int restart_flag;
     if (tid == 0) restart_flag = 0;
 
-    const float tau_raw = kTauLog2 / kLog2e;
+    const float tau_raw = tau_log2<T> / kLog2e;
     // m_true: exact running max of this lane's latent; m_ref: the reference
     // of the weights, fixed for a pass (set on the first tile of the first
     // pass, raised to m_true when a pass restarts).

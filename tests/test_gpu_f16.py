@@ -100,8 +100,11 @@ def test_splitk_long_input(cw, oracle, bf16):
 @pytest.mark.parametrize("bf16", [False, True], ids=["fp16", "bf16"])
 def test_growing_scores_force_restarts(cw, oracle, bf16):
     """Scores rise by ~0.43 per key (~124 in exp2 units over the row), far past
-    the reference the weights are taken against, so every row restarts its
-    pass over the keys at least once."""
+    the reference the weights are taken against.  launch_wmma_kernel splits
+    these 200 keys over workgroups at this shape, so the inputs also run
+    through the split-K entry with one split: one workgroup walks all seven
+    tiles and, in key order, restarts its pass (twice for fp16, whose weights
+    are bounded by 2^15)."""
     rng = np.random.RandomState(8)
     nl, ni = 40, 200
     u = rng.randn(768)
@@ -113,6 +116,10 @@ def test_growing_scores_force_restarts(cw, oracle, bf16):
     v = rng.randn(1, ni, 768).astype(np.float32)
     for perm in (rng.permutation(ni), np.arange(ni)):
         kp, vp = k[:, perm], v[:, perm]
+        ref = _rounded_ref(oracle, cw, q, kp, vp, bf16)
         out = _run(cw, q, kp, vp, bf16)
-        tight = oracle.rel_err(out, _rounded_ref(oracle, cw, q, kp, vp, bf16))
+        tight = oracle.rel_err(out, ref)
         assert np.all(np.isfinite(out)) and tight <= 2 * TIGHT[bf16], tight
+        one, _ = cw.wmma_splitk_partials(q, kp, vp, 1, nl, ni, 768, 1, bf16=bf16)
+        tight = oracle.rel_err(one, ref)
+        assert np.all(np.isfinite(one)) and tight <= 2 * TIGHT[bf16], tight

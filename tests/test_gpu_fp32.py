@@ -73,7 +73,10 @@ def test_config3_batched_sweep(cw, oracle, b):
 
 def test_growing_scores_force_rescales(cw, oracle):
     """Scores rise by ~12 per key across the key axis, so the running max grows
-    far past the lazy-rescale threshold many times within one row."""
+    far past the lazy-rescale threshold many times within one row.  At this
+    shape launch_optimized_kernel splits the keys over workgroups, so the same
+    inputs also run through launch_splitk_kernel with one split: one workgroup
+    walks all 200 keys and must rescale on the way."""
     rng = np.random.RandomState(8)
     nl, ni = 40, 200
     u = rng.randn(768)
@@ -90,6 +93,10 @@ def test_growing_scores_force_rescales(cw, oracle):
     k_sorted = k[:, np.argsort(k[0] @ u)]
     v_sorted = v[:, np.argsort(k[0] @ u)]
     fp32_gate(_events(cw, "vectorized", q, k_sorted, v_sorted), ref)
+    for kk, vv in ((k, v), (k_sorted, v_sorted)):
+        out, (po, pm, pl) = cw.splitk_partials(q, kk, vv, 1, nl, ni, 768, 1)
+        fp32_gate(out, ref)
+        fp32_gate(po.reshape(out.shape) / pl.reshape(1, nl, 1), ref)
 
 
 def test_special_cases(cw, oracle):
