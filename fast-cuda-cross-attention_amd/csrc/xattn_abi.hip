@@ -2,6 +2,7 @@
 // queries, workspace and launch planning.  The kernels live in the other
 // translation units; every launcher here is host code only.
 #include <stdarg.h>
+#include <stdint.h>
 #include <stdio.h>
 #include <string.h>
 
@@ -133,6 +134,22 @@ bool validate_dim768(const char* who, int dim) {
         set_error(XATTN_ERR_UNSUPPORTED, "%s: dim=%d unsupported (built for dim=%d)", who, dim,
                   kDim);
         return false;
+    }
+    return true;
+}
+
+// The MFMA paths move Q/K/V and the fp32 rows in 16-byte vectors (and K/V by
+// 16-byte global->LDS DMA); hipMalloc returns 256-byte aligned memory.
+bool validate_aligned16(const char* who, const void* Q, const void* K, const void* V,
+                        const void* out, const void* po) {
+    const void* ptr[5] = {Q, K, V, out, po};
+    const char* name[5] = {"Q", "K", "V", "output", "partial output"};
+    for (int i = 0; i < 5; ++i) {
+        if ((reinterpret_cast<uintptr_t>(ptr[i]) & 15) != 0) {
+            set_error(XATTN_ERR_INVALID_VALUE, "%s: %s pointer %p is not 16-byte aligned", who,
+                      name[i], ptr[i]);
+            return false;
+        }
     }
     return true;
 }
@@ -275,6 +292,7 @@ void launch_optimized_kernel(const float* Q, const float* K, const float* V, flo
     const char* who = "launch_optimized_kernel";
     if (!validate_common(who, Q, K, V, output, batch_size, N_latent, N_input, dim)) return;
     if (!validate_dim768(who, dim)) return;
+    if (!validate_aligned16(who, Q, K, V, output, nullptr)) return;
     if (batch_size == 0 || N_latent == 0) return;
     const int S = optimized_num_splits(batch_size, N_latent, N_input, device_cu_count());
     if (S <= 1) {
@@ -299,6 +317,7 @@ void launch_splitk_kernel(const float* Q, const float* K, const float* V, float*
     if (!validate_common(who, Q, K, V, output, batch_size, N_latent, N_input, dim)) return;
     if (!validate_dim768(who, dim)) return;
     if (!validate_splits(who, po, pm, pl, batch_size, N_latent, num_splits)) return;
+    if (!validate_aligned16(who, Q, K, V, output, po)) return;
     if (batch_size == 0 || N_latent == 0) return;
     if ((long long)batch_size * N_latent * num_splits > 0x7fffffffLL) {
         set_error(XATTN_ERR_INVALID_VALUE, "%s: B*NL*num_splits too large", who);
@@ -317,6 +336,7 @@ static void wmma_common(bool bf16, const char* who, const uint16_t* Q, const uin
                         int N_input, int dim, hipStream_t stream) {
     if (!validate_common(who, Q, K, V, output, batch_size, N_latent, N_input, dim)) return;
     if (!validate_dim768(who, dim)) return;
+    if (!validate_aligned16(who, Q, K, V, output, nullptr)) return;
     if (batch_size == 0 || N_latent == 0) return;
     const int S = plan_splits(batch_size, N_latent, N_input, device_cu_count(), 64, 32);
     if (S <= 1) {
@@ -341,6 +361,7 @@ static void wmma_splitk_common(bool bf16, const char* who, const uint16_t* Q, co
     if (!validate_common(who, Q, K, V, output, batch_size, N_latent, N_input, dim)) return;
     if (!validate_dim768(who, dim)) return;
     if (!validate_splits(who, po, pm, pl, batch_size, N_latent, num_splits)) return;
+    if (!validate_aligned16(who, Q, K, V, output, po)) return;
     if (batch_size == 0 || N_latent == 0) return;
     if ((long long)batch_size * N_latent * num_splits > 0x7fffffffLL) {
         set_error(XATTN_ERR_INVALID_VALUE, "%s: B*NL*num_splits too large", who);

@@ -125,6 +125,32 @@ __device__ inline void dma16(const void* gptr, void* lds_base) {
         gptr, (__attribute__((address_space(3))) void*)lds_base, 16, 0, 0);
 }
 
+// Byte address of an LDS location (the value M0 takes for an LDS DMA).
+__device__ inline unsigned lds_u32(const void* p) {
+    return (unsigned)(uintptr_t)((const __attribute__((address_space(3))) char*)p);
+}
+
+// The same DMA issued as inline assembly: lane i reads sbase + voff_i (sbase
+// wave-uniform, in SGPRs) and writes LDS bytes [lds_byte + 16 i, +16).  The
+// compiler does not see it, so it inserts no vmcnt waits of its own before
+// later LDS reads (it drains every outstanding DMA before a transposing LDS
+// read, and before any LDS read once a kernel has more than one LDS object);
+// the caller orders it with wait_vmcnt + lds_barrier, which count it like any
+// vector memory load.  M0 (reserved to the compiler) is saved and restored
+// around the load and written one wait state before the load reads it.
+__device__ inline void dma16_untracked(const void* sbase, unsigned voff, unsigned lds_byte) {
+    unsigned saved;
+    asm volatile(
+        "s_mov_b32 %0, m0\n\t"
+        "s_mov_b32 m0, %3\n\t"
+        "s_nop 0\n\t"
+        "global_load_lds_dwordx4 %1, %2\n\t"
+        "s_mov_b32 m0, %0"
+        : "=&s"(saved)
+        : "v"(voff), "s"(sbase), "s"(lds_byte)
+        : "memory");
+}
+
 }  // namespace xattn
 
 // --------------------------------------------------------------------------
