@@ -133,6 +133,21 @@ def test_validation_refuses_before_launch(cw):
     assert code == 1 and "num_splits" in msg
     code, msg = _call(cw, "launch_tiled_kernel", dummy, dummy, dummy, dummy, 1, 4, 4, 769, s0)
     assert code == 2
+    # the MFMA paths move rows in 16-byte vectors: every operand must be aligned
+    odd = ctypes.cast(ctypes.c_void_p(0x1004), F)
+    code, msg = _call(cw, "launch_optimized_kernel", dummy, odd, dummy, dummy, 1, 64, 784, 768,
+                      s0)
+    assert code == 1 and "K pointer" in msg and "16-byte" in msg
+    P = ctypes.c_void_p
+    code, msg = _call(cw, "launch_wmma_splitk_bf16_kernel", P(0x1000), P(0x1000), P(0x1000),
+                      dummy, odd, dummy, dummy, 1, 64, 784, 768, 2, s0)
+    assert code == 1 and "partial output" in msg
+    code, msg = _call(cw, "launch_wmma_kernel", P(0x1002), P(0x1000), P(0x1000), dummy, 1, 64,
+                      784, 768, s0)
+    assert code == 1 and "Q pointer" in msg
+    # the scalar rungs take any float pointer
+    code, _ = _call(cw, "launch_tiled_kernel", dummy, dummy, dummy, dummy, 0, 4, 4, 768, s0)
+    assert code == 0
     # the error is cleared once read
     assert cw.lib.xattn_get_last_error() == 0
     # empty problems are a no-op, not an error
