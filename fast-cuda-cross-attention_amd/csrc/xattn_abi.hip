@@ -230,6 +230,18 @@ int xattn_device_info(int device, int* cu_count, int* lds_bytes_per_block) {
     return 0;
 }
 
+int xattn_device_arch(int device, char* arch, int arch_len, int* clock_khz) {
+    hipDeviceProp_t prop;
+    const hipError_t e = hipGetDeviceProperties(&prop, device);
+    if (e != hipSuccess) return (int)e;
+    if (arch && arch_len > 0) {
+        strncpy(arch, prop.gcnArchName, (size_t)arch_len - 1);
+        arch[arch_len - 1] = '\0';
+    }
+    if (clock_khz) *clock_khz = prop.clockRate;
+    return 0;
+}
+
 int xattn_xcd_remap(int block, int num_blocks) { return xcd_remap(block, num_blocks); }
 
 int xattn_optimized_num_splits(int batch_size, int N_latent, int N_input, int cu_count) {

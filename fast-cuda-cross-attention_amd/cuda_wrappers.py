@@ -136,6 +136,8 @@ lib.xattn_get_last_error_string.argtypes = []
 lib.xattn_get_last_error_string.restype = ctypes.c_char_p
 lib.xattn_device_info.argtypes = [_I, ctypes.POINTER(_I), ctypes.POINTER(_I)]
 lib.xattn_device_info.restype = ctypes.c_int
+lib.xattn_device_arch.argtypes = [_I, ctypes.c_char_p, _I, ctypes.POINTER(_I)]
+lib.xattn_device_arch.restype = ctypes.c_int
 lib.xattn_xcd_remap.argtypes = [_I, _I]
 lib.xattn_xcd_remap.restype = ctypes.c_int
 lib.xattn_optimized_num_splits.argtypes = [_I, _I, _I, _I]
@@ -212,6 +214,17 @@ def device_info(device=0):
     if err != 0:
         raise RuntimeError(f"xattn_device_info failed with HIP error {err}")
     return cu.value, lds.value
+
+
+def device_arch(device=0):
+    """(architecture name, e.g. 'gfx950:sramecc+:xnack-', peak clock in kHz)
+    of ``device``."""
+    buf = ctypes.create_string_buffer(256)
+    khz = ctypes.c_int(0)
+    err = lib.xattn_device_arch(device, buf, len(buf), ctypes.byref(khz))
+    if err != 0:
+        raise RuntimeError(f"xattn_device_arch failed with HIP error {err}")
+    return buf.value.decode(errors="replace"), khz.value
 
 
 def _max_smem_optin(device=0):

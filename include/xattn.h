@@ -129,6 +129,14 @@ const char* xattn_get_last_error_string(void);
  * workgroup may use.  Returns a hipError_t value (0 on success). */
 int xattn_device_info(int device, int* cu_count, int* lds_bytes_per_block);
 
+/* Additive (no reference counterpart; the reference names its GPU from
+ * nvidia-smi, experiments/gpu_specs.py:60-109): the device's architecture
+ * name as the HIP runtime reports it (e.g. "gfx950:sramecc+:xnack-"), NUL
+ * terminated within arch_len bytes, and its peak engine clock in kHz.  The
+ * product name alone does not identify the part on hosts without libdrm's
+ * ASIC table.  Returns a hipError_t value (0 on success). */
+int xattn_device_arch(int device, char* arch, int arch_len, int* clock_khz);
+
 /* Host copies of the launch planning, for inspection and tests. */
 int xattn_xcd_remap(int block, int num_blocks);
 /* Number of key splits launch_optimized_kernel uses internally. */

@@ -1,0 +1,129 @@
+"""The experiment drivers end to end on the GPU, at small sizes: every row
+they log must be 'ok' against the float32 references they read."""
+
+import math
+import os
+import sys
+
+import numpy as np
+import pytest
+
+from conftest import PKG
+
+EXP = os.path.join(PKG, "experiments")
+if EXP not in sys.path:
+    sys.path.insert(0, EXP)
+
+pytestmark = pytest.mark.gpu
+
+
+def _rows(path):
+    import csvlog
+    return csvlog.read_rows(path)
+
+
+def test_ni_sweep_all_kernels(tmp_path, monkeypatch, cw):
+    import bench_perceiver_ni
+    import gen_perceiver_refs as gpr
+    monkeypatch.chdir(tmp_path)
+    for ni in (100, 784):
+        gpr.write_case(str(tmp_path / "data"), 16, ni)
+    impls = ["naive", "warp", "tiled", "vectorized", "splitk", "wmma", "wmma_splitk",
+             "wmma_bf16", "wmma_splitk_bf16"]
+    csv_path = str(tmp_path / "ni.csv")
+    rc = bench_perceiver_ni.main(["--n-latent", "16", "--n-input", "100", "784", "--impls",
+                                  *impls, "--warmup", "1", "--iters", "2", "--data",
+                                  str(tmp_path / "data"), "--csv", csv_path])
+    assert rc == 0
+    rows = _rows(csv_path)
+    assert len(rows) == 2 * len(impls)
+    for r in rows:
+        assert r["status"] == "ok", r
+        assert r["gpu"] and float(r["latency_ms_mean"]) > 0
+        if r["impl"].startswith(("splitk", "wmma_splitk")):
+            assert r["note"].startswith("splits=")
+    assert {r["precision"] for r in rows} == {"fp32", "fp16", "bf16"}
+
+
+def test_nl_sweep_records_occupancy(tmp_path, monkeypatch, cw):
+    import bench_perceiver_nl
+    import gen_perceiver_refs as gpr
+    monkeypatch.chdir(tmp_path)
+    for nl in (4, 64):
+        gpr.write_case(str(tmp_path / "data"), nl, 300)
+    csv_path = str(tmp_path / "nl.csv")
+    rc = bench_perceiver_nl.main(["--n-input", "300", "--n-latent", "4", "64", "--impls",
+                                  "warp", "tiled", "vectorized", "--warmup", "1", "--iters",
+                                  "2", "--data", str(tmp_path / "data"), "--csv", csv_path])
+    assert rc == 0
+    rows = _rows(csv_path)
+    assert [r["status"] for r in rows] == ["ok"] * 6
+    warp4 = next(r for r in rows if r["impl"] == "warp" and r["N_latent"] == "4")
+    assert "blocks=1" in warp4["note"] and "act_cu=1" in warp4["note"]
+
+
+def test_wmma_comparison(tmp_path, monkeypatch, cw):
+    import bench_wmma
+    import gen_perceiver_refs as gpr
+    monkeypatch.chdir(tmp_path)
+    gpr.write_case(str(tmp_path / "data"), 64, 784)
+    csv_path = str(tmp_path / "e7.csv")
+    rc = bench_wmma.main(["--n-latent", "64", "--n-input", "784", "--impls", "wmma",
+                          "wmma_bf16", "wmma_splitk_bf16", "--warmup", "1", "--iters", "2",
+                          "--data", str(tmp_path / "data"), "--csv", csv_path])
+    assert rc == 0
+    rows = _rows(csv_path)
+    assert [r["impl"] for r in rows] == ["vectorized", "wmma", "wmma_bf16", "wmma_splitk_bf16"]
+    assert all(r["status"] == "ok" for r in rows), rows
+    assert float(rows[1]["rel_err"]) < 2e-3 and float(rows[2]["rel_err"]) < 1e-2
+
+
+def test_sdpa_math_matches_oracle(oracle):
+    from sdpa_bench import benchmark_sdpa_events
+    rng = np.random.RandomState(5)
+    q = rng.randn(2, 24, 768).astype(np.float32)
+    k = rng.randn(2, 70, 768).astype(np.float32)
+    v = rng.randn(2, 70, 768).astype(np.float32)
+    ref = oracle.attention_f64(q, k, v)
+    out, mean_ms, _ = benchmark_sdpa_events(q, k, v, 2, 24, 70, 768, "math", "fp32", 1, 2)
+    assert out.shape == (2, 24, 768) and mean_ms > 0
+    assert oracle.rel_err(out, ref) < 1e-5
+    # the spelled-out 16-bit materialized product
+    for prec, tol in (("fp16", 5e-3), ("bf16", 2e-2)):
+        out, _, _ = benchmark_sdpa_events(q, k, v, 2, 24, 70, 768, "math", prec, 1, 2)
+        assert np.all(np.isfinite(out)) and oracle.rel_err(out, ref) < tol, prec
+
+
+def test_sdpa_backend_probe_runs_math():
+    import e0_sdpa_backend
+    res = e0_sdpa_backend.probe(16, 64, 1, 2)
+    assert len(res) == 8
+    by = {(impl, prec): (status, note) for impl, prec, status, _, _, note in res}
+    assert by[("sdpa_math", "fp32")][0] == "ok"
+    assert by[("sdpa_math", "bf16")][0] == "ok"
+    for status, note in by.values():
+        assert status in ("ok", "unsupported") and (status == "ok" or note)
+
+
+def test_anchor_comparison_table(tmp_path, monkeypatch, cw):
+    import compare_sdpa
+    monkeypatch.chdir(tmp_path)
+    md = str(tmp_path / "anchor.md")
+    rc = compare_sdpa.main(["--n-latent", "32", "--n-input", "256", "--warmup", "1",
+                            "--iters", "2", "--impls", "sdpa_math", "vectorized", "splitk",
+                            "wmma_bf16", "--csv", str(tmp_path / "a.csv"), "--md", md])
+    assert rc == 0
+    text = open(md).read()
+    for impl in ("sdpa_math", "vectorized", "splitk", "wmma_bf16"):
+        assert f"| {impl} |" in text, text
+    rows = _rows(str(tmp_path / "a.csv"))
+    assert all(r["status"] == "ok" for r in rows), rows
+    assert math.isclose(float(next(r for r in rows if r["impl"] == "sdpa_math")["rel_err"]), 0,
+                        abs_tol=1e-5)
+
+
+def test_device_detection(cw):
+    import gpu_specs
+    arch, khz = cw.device_arch()
+    assert arch.split(":")[0] == "gfx950" and khz > 1_000_000
+    assert gpu_specs.detect_gpu_name() in ("MI355X", "MI350X")
