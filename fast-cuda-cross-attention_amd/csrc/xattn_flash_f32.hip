@@ -12,9 +12,11 @@
 // S[q = j][key = 4g + i] in accumulator register i -- exactly the A-operand
 // layout P[q = j][k = g] of the P.V MFMA for k-slab i, so P never moves.
 //
-// Registers per lane: Q^T operand 192 (Q[q0+j][16u + 4g + c], u < 48, c < 4),
-// O accumulator 192 (O[q0 + 4g + i][64T + 4j + c], T < 12), a few dozen more.
-// One wavefront per SIMD; the MFMA pipe is kept busy by a single wave.
+// Registers per lane: Q^T operand 192 VGPRs (Q[q0+j][16u + 4g + c], u < 48,
+// c < 4), O accumulator 192 AGPRs (O[q0 + 4g + i][64T + 4j + c], T < 12),
+// written only by MFMA, so neither operand is ever copied between register
+// files inside the loop.  One wavefront per SIMD; the MFMA pipe is kept busy
+// by a single wave.
 //
 // K and V tiles are shared by the 4 wavefronts through LDS and arrive by
 // global->LDS DMA (16 B per lane, 1 KiB per wave instruction).  Phases
@@ -22,13 +24,16 @@
 // p + 2 is requested at the start of phase p, so every tile has two phases
 // (~12k cycles) to arrive.  One barrier per phase.
 //
-// Softmax keeps the running max in raw dot-product units.  The accumulator
-// is only rescaled when a latent's tile max exceeds the max in use by more
-// than 2^8 in exp2 space (weights stay <= 256, no overflow), which for
-// unit-variance scores happens only on the first tile.  The exact max is
-// tracked separately and folded in at the end, so the normalised output and
-// the split partials (pm = exact max score) match the reference algorithm
-// (kernel_vectorized.cu:277-181, kernel_splitk.cu:94-180).
+// Softmax in raw dot-product units by passes: a row's weights are
+// exp2((s - m_ref) c2) with m_ref fixed for the whole pass (the row max of
+// the first tile), so the accumulator is never rescaled.  If a later score
+// exceeds m_ref by 2^64 in exp2 space the workgroup abandons the pass (a
+// flag in LDS, read by every wavefront after the same barrier) and runs the
+// keys again with m_ref = the max seen so far; unit-variance scores never
+// need a second pass.  The exact max is tracked separately and folded in at
+// the end, so the normalised output and the split partials (pm = exact max
+// score) match the reference algorithm (kernel_vectorized.cu:277-181,
+// kernel_splitk.cu:94-180).
 
 #include "xattn_common.h"
 
@@ -45,10 +50,11 @@ constexpr int NBUF = 3;
 constexpr int CHUNKS = BN * kDim / (kWave * 4);  // 1 KiB DMA chunks per tile (48)
 constexpr int CPW = CHUNKS / NW;                 // per wavefront (12)
 constexpr int ROW_CHUNKS = kDim / (kWave * 4);   // 3 chunks per key row
-constexpr float kTauLog2 = 8.0f;
+// a pass restarts when a score exceeds its reference by 2^kTauLog2 (exp2 units)
+constexpr float kTauLog2 = 64.0f;
 
 static_assert(CHUNKS % NW == 0, "chunks per wave");
-static_assert(NBUF * BUF * 4 <= 160 * 1024, "LDS budget");
+static_assert((NBUF * BUF + 4) * 4 <= 160 * 1024, "LDS budget");
 
 struct Params {
     const float* Q;
@@ -68,7 +74,8 @@ __device__ inline f4 mfma4(float a, float b, f4 c) {
 template <bool PARTIAL>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1)))
 void flash_f32_kernel(Params p) {
-    __shared__ __attribute__((aligned(16))) float lds[NBUF * BUF];
+    // tile buffers, then the restart flag (one LDS object)
+    __shared__ __attribute__((aligned(16))) float lds[NBUF * BUF + 4];
 
     const int item = xcd_remap(blockIdx.x, gridDim.x);
     const int rb = item % p.row_blocks;
@@ -112,6 +119,10 @@ void flash_f32_kernel(Params p) {
     const float* Kb = p.K + (size_t)b * p.NI * kDim;
     const float* Vb = p.V + (size_t)b * p.NI * kDim;
     const int ntiles = (k1 - k0 + BN - 1) / BN;
+    // Non-empty (the early return above); without this the compiler guards
+    // the tile loop for zero trips and the split-K instantiation spills.
+    __builtin_assume(k1 - k0 >= 1);
+    __builtin_assume(ntiles >= 1);
     const int nphase = 2 * ntiles;
 
     // Phase ph (even: K of tile ph/2, odd: V of tile ph/2) -> buffer ph % 3.
@@ -157,108 +168,121 @@ void flash_f32_kernel(Params p) {
     issue(0);
     issue(1);
 
-    f4 acc[12][4];
-#pragma unroll
-    for (int T = 0; T < 12; ++T)
-#pragma unroll
-        for (int c = 0; c < 4; ++c) acc[T][c] = (f4){0.f, 0.f, 0.f, 0.f};
-
+    // The flag lives in the tile array: a second LDS object would give the
+    // LDS reads alias-scope metadata and make the compiler drain the DMA
+    // before each of them.
+    int* restart_flag = (int*)(lds + NBUF * BUF);
+    if (tid == 0) *restart_flag = 0;
     const float c2 = kLog2e / sqrtf((float)kDim);
     const float tau_raw = kTauLog2 / c2;
-    float m_true = -FLT_MAX, m_used = -FLT_MAX, lsum = 0.f;
+    float m_true = -FLT_MAX, m_ref = -FLT_MAX, lsum;
+    f4 acc[12][4];
 
-    for (int tile = 0; tile < ntiles; ++tile) {
-        const int n0 = k0 + tile * BN;
-        int ph = 2 * tile;
-
-        // ---------------- QK phase ----------------
-        wait_vmcnt<CPW>();      // this phase landed; phase ph+1 may be in flight
-        lds_barrier();
-        if (ph + 2 < nphase) issue(ph + 2);
-        f4 s;
-        {
-            // K operand reads run two 4-MFMA groups ahead; the sched_barrier
-            // keeps the scheduler from hoisting all 48 reads (192 VGPRs).
-            const float* kb = lds + (ph % NBUF) * BUF + j * ROW + 4 * g;
-            f4 s0 = {0.f, 0.f, 0.f, 0.f}, s1 = s0;
-            f4 kv[3];
-            kv[0] = *(const f4*)(kb);
-            kv[1] = *(const f4*)(kb + 16);
-#pragma unroll
-            for (int u = 0; u < 48; ++u) {
-                if (u + 2 < 48) kv[(u + 2) % 3] = *(const f4*)(kb + 16 * (u + 2));
-                const f4 k4 = kv[u % 3];
-                s0 = mfma4(k4[0], qr[u][0], s0);
-                s1 = mfma4(k4[1], qr[u][1], s1);
-                s0 = mfma4(k4[2], qr[u][2], s0);
-                s1 = mfma4(k4[3], qr[u][3], s1);
-                __builtin_amdgcn_sched_barrier(0);
-            }
-            s = s0 + s1;
+    for (bool first = true;; first = false) {  // passes over the keys; a second is rare
+        if (!first) {
+            issue(0);
+            issue(1);
         }
+#pragma unroll
+        for (int T = 0; T < 12; ++T)
+#pragma unroll
+            for (int c = 0; c < 4; ++c) acc[T][c] = (f4){0.f, 0.f, 0.f, 0.f};
+        lsum = 0.f;
+        bool restart = false;
+        for (int tile = 0; tile < ntiles; ++tile) {
+            const int n0 = k0 + tile * BN;
+            int ph = 2 * tile;
 
-        // ---------------- online softmax ----------------
-        float x[4];
+            // ---------------- QK phase ----------------
+            wait_vmcnt<CPW>();      // this phase landed; phase ph+1 may be in flight
+            lds_barrier();
+            if (ph + 2 < nphase) issue(ph + 2);
+            f4 s;
+            {
+                // K operand reads run two 4-MFMA groups ahead; the sched_barrier
+                // keeps the scheduler from hoisting all 48 reads (192 VGPRs).
+                const float* kb = lds + (ph % NBUF) * BUF + j * ROW + 4 * g;
+                f4 s0 = {0.f, 0.f, 0.f, 0.f}, s1 = s0;
+                f4 kv[3];
+                kv[0] = *(const f4*)(kb);
+                kv[1] = *(const f4*)(kb + 16);
 #pragma unroll
-        for (int i = 0; i < 4; ++i) x[i] = (n0 + 4 * g + i < k1) ? s[i] : -INFINITY;
-        float tmax = fmaxf(fmaxf(x[0], x[1]), fmaxf(x[2], x[3]));
-        tmax = wave_max16_groups(tmax);
-        m_true = fmaxf(m_true, tmax);
-        const bool grow = tmax > m_used + tau_raw;
-        if (__any(grow)) {
-            const float m_new = grow ? tmax : m_used;
-            const float alpha = fast_exp2((m_used - m_new) * c2);
-            lsum *= alpha;
-            m_used = m_new;
-            float a[4];
-#pragma unroll
-            for (int i = 0; i < 4; ++i) a[i] = __shfl(alpha, 4 * g + i);
-#pragma unroll
-            for (int T = 0; T < 12; ++T)
-#pragma unroll
-                for (int c = 0; c < 4; ++c)
-#pragma unroll
-                    for (int i = 0; i < 4; ++i) acc[T][c][i] *= a[i];
-        }
-        float pw[4];
-        float rs = 0.f;
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            pw[i] = fast_exp2((x[i] - m_used) * c2);
-            rs += pw[i];
-        }
-        lsum += wave_sum16_groups(rs);
-
-        // ---------------- PV phase ----------------
-        ph += 1;
-        if (ph + 1 < nphase) wait_vmcnt<CPW>();
-        else wait_vmcnt<0>();
-        lds_barrier();
-        if (ph + 2 < nphase) issue(ph + 2);
-        {
-            // Group n = 12 r + T: V[4g + r][64T + 4j .. +3] feeds the four
-            // MFMAs of output tiles (T, c = 0..3) for k-slab r.
-            const float* vb = lds + (ph % NBUF) * BUF + 4 * j + 4 * g * ROW;
-            f4 vv[3];
-            vv[0] = *(const f4*)(vb);
-            vv[1] = *(const f4*)(vb + 64);
-#pragma unroll
-            for (int n = 0; n < 48; ++n) {
-                if (n + 2 < 48) {
-                    const int rn = (n + 2) / 12, tn = (n + 2) % 12;
-                    vv[(n + 2) % 3] = *(const f4*)(vb + rn * ROW + 64 * tn);
+                for (int u = 0; u < 48; ++u) {
+                    if (u + 2 < 48) kv[(u + 2) % 3] = *(const f4*)(kb + 16 * (u + 2));
+                    const f4 k4 = kv[u % 3];
+                    s0 = mfma4(k4[0], qr[u][0], s0);
+                    s1 = mfma4(k4[1], qr[u][1], s1);
+                    s0 = mfma4(k4[2], qr[u][2], s0);
+                    s1 = mfma4(k4[3], qr[u][3], s1);
+                    __builtin_amdgcn_sched_barrier(0);
                 }
-                const int r = n / 12, T = n % 12;
-                const f4 v4 = vv[n % 3];
+                s = s0 + s1;
+            }
+
+            // ---------------- online softmax ----------------
+            float x[4];
 #pragma unroll
-                for (int c = 0; c < 4; ++c) acc[T][c] = mfma4(pw[r], v4[c], acc[T][c]);
-                __builtin_amdgcn_sched_barrier(0);
+            for (int i = 0; i < 4; ++i) x[i] = (n0 + 4 * g + i < k1) ? s[i] : -INFINITY;
+            float tmax = fmaxf(fmaxf(x[0], x[1]), fmaxf(x[2], x[3]));
+            tmax = wave_max16_groups(tmax);
+            m_true = fmaxf(m_true, tmax);
+            if (m_ref == -FLT_MAX) m_ref = tmax;
+            if (__any(tmax > m_ref + tau_raw) && lane == 0) *restart_flag = 1;
+            float pw[4];
+            float rs = 0.f;
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                pw[i] = fast_exp2((x[i] - m_ref) * c2);
+                rs += pw[i];
+            }
+            lsum += wave_sum16_groups(rs);
+
+            // ---------------- PV phase ----------------
+            ph += 1;
+            if (ph + 1 < nphase) wait_vmcnt<CPW>();
+            else wait_vmcnt<0>();
+            lds_barrier();
+            // Every wavefront sets the flag (if at all) before this barrier,
+            // so all of them leave the pass at the same tile.
+            if (__builtin_amdgcn_readfirstlane(*restart_flag)) {
+                restart = true;
+                break;
+            }
+            if (ph + 2 < nphase) issue(ph + 2);
+            {
+                // Group n = 12 r + T: V[4g + r][64T + 4j .. +3] feeds the four
+                // MFMAs of output tiles (T, c = 0..3) for k-slab r.
+                const float* vb = lds + (ph % NBUF) * BUF + 4 * j + 4 * g * ROW;
+                f4 vv[3];
+                vv[0] = *(const f4*)(vb);
+                vv[1] = *(const f4*)(vb + 64);
+#pragma unroll
+                for (int n = 0; n < 48; ++n) {
+                    if (n + 2 < 48) {
+                        const int rn = (n + 2) / 12, tn = (n + 2) % 12;
+                        vv[(n + 2) % 3] = *(const f4*)(vb + rn * ROW + 64 * tn);
+                    }
+                    const int r = n / 12, T = n % 12;
+                    const f4 v4 = vv[n % 3];
+#pragma unroll
+                    for (int c = 0; c < 4; ++c) acc[T][c] = mfma4(pw[r], v4[c], acc[T][c]);
+                    __builtin_amdgcn_sched_barrier(0);
+                }
             }
         }
+        if (!restart) break;
+        // Some latent's scores outgrew its reference: drain the DMA (phases up
+        // to ph + 2 may be in flight), clear the flag, and run the keys again
+        // with the reference raised to the max seen so far.
+        wait_vmcnt<0>();
+        lds_barrier();
+        if (tid == 0) *restart_flag = 0;
+        m_ref = m_true;
+        lds_barrier();
     }
 
-    // Fold the exact max back in: factor = exp(m_used - m_true) <= 1.
-    const float factor = fast_exp2((m_used - m_true) * c2);
+    // Fold the exact max back in: factor = exp(m_ref - m_true) <= 1.
+    const float factor = fast_exp2((m_ref - m_true) * c2);
     float rowscale;
     if (PARTIAL) rowscale = factor;
     else rowscale = factor / (lsum * factor + 1e-6f);
