@@ -32,19 +32,18 @@
 // The O^T accumulator puts O[q = j][d + 4g .. d + 4g + 3] in lane (j, g): one
 // 16-byte store per (latent block, column block).
 //
-// Tiles in LDS are fragment-major: every MFMA operand read is one contiguous
-// run indexed by the lane, so each read is a base register plus an immediate
-// offset (no per-read address arithmetic: a wave64 VALU instruction holds its
-// SIMD for four cycles, which is what the MFMA sections would wait on) and
-// the reads are conflict-free.
-//   K tile: fragment (key half kh, 32-column group c) at (24 kh + c) KiB;
-//           lane 16g + j at +16 lanes holds K[16kh + j][32c + 8g .. +7].
-//   V tile: piece (key half kh, 16-column block c) at (48 kh + c) * 512 B;
-//           lane 16g + 4e + q at +8 lanes holds V[16kh + 4g + e][16c + 4q .. +3].
-// The global->LDS DMA does the gather: each 1 KiB chunk is 16 rows x 64 bytes
-// of the row-major K or V (chunk n of a tile lies at n KiB for both).  K and
-// V tiles (48 KiB each) share one pipeline: phases alternate QK(t) / PV(t),
-// phase p reads buffer p % 3 and requests phase p + 2; 3 buffers = 144 KiB.
+// Tiles in LDS are row-major with a 1568-byte row stride (1536 bytes of data
+// and 32 of padding).  A stride of 32 mod 512 bytes spreads the 16 rows of a
+// K fragment read and the 16 rows of a transposed V read over distinct banks
+// (measured at the rate of a plain sequential read), and every MFMA operand
+// read is one per-lane base register plus an immediate offset: a wave64 VALU
+// instruction holds its SIMD for four cycles, so per-read address arithmetic
+// would cost the MFMA sections more than the reads themselves.  The tile
+// (32 rows, 49 KiB) is filled by 49 global->LDS DMA chunks of 1 KiB whose
+// lanes read consecutive 16-byte pieces of a row (coalesced; the lanes that
+// land on padding re-read the row's last piece).  K and V tiles share one
+// pipeline: phases alternate QK(t) / PV(t), phase p reads buffer p % 3 and
+// requests phase p + 2; 3 buffers = 147 KiB.
 #include "xattn_common.h"
 
 namespace xattn {
@@ -61,21 +60,21 @@ constexpr int CBW = NCB / NH;          // latent blocks per wavefront (2)
 constexpr int DW = kDim / NA;          // columns of D per wavefront (192)
 constexpr int KS = DW / 32;            // k-steps of a score MFMA chain (6)
 constexpr int DB = DW / 16;            // 16-column output blocks per wavefront (12)
-constexpr int ROWB = kDim * 2;         // bytes per K / V row (1536)
-constexpr int BUFB = BN * ROWB;        // bytes per tile buffer (48 KiB)
+constexpr int ROWB = kDim * 2;         // bytes per K / V row in memory (1536)
+constexpr int LROW = ROWB + 32;        // bytes per tile row in LDS (1568)
+constexpr int BUFB = BN * LROW;        // bytes per tile buffer (49 KiB)
 constexpr int NBUF = 3;
-constexpr int CHUNKS = BUFB / 1024;        // 1 KiB DMA chunks per tile (48)
-constexpr int CPW = CHUNKS / NW;           // per wavefront (6)
+constexpr int CHUNKS = BUFB / 1024;        // 1 KiB DMA chunks per tile (49)
+constexpr int CPW = CHUNKS / NW;           // per wavefront (6); wavefront 0 also issues the last
 constexpr int NUNIT = NCB * 2;             // (latent block, key half) softmax units (8)
 constexpr int KPF = 4;                     // K fragments read ahead of their MFMAs
 constexpr int VPF = 3;                     // V column blocks read ahead of their MFMAs
 
 static_assert(NUNIT == NW, "one softmax unit per wavefront");
-static_assert(CHUNKS % NW == 0, "DMA split");
 static_assert(NBUF * BUFB + NCB * kWave * 16 + NW * QB * 8 + NCB * QB * 4 + 4 <= 160 * 1024,
               "LDS budget");
 static_assert(NUNIT * NA * kWave * 16 <= BUFB, "score exchange fits in a tile buffer");
-static_assert(CPW * NA == 24 && NW == 2 * NA, "a wavefront's chunks: one key half, 6 column groups");
+static_assert(CHUNKS * 1024 == BUFB && CHUNKS == CPW * NW + 1, "DMA split");
 
 // A row's weights are exp2(s - m_ref) with m_ref fixed for a whole pass over
 // the keys; a pass restarts when some score exceeds m_ref by tau_log2<T> (in
@@ -200,41 +199,54 @@ void flash16_kernel(Params p) {
     __builtin_assume(nk >= 1);
     const int ntiles = (nk + BN - 1) / BN;
     __builtin_assume(ntiles >= 1);
-    const int nphase = 2 * ntiles;
 
-    // DMA.  Wavefront w fills chunks 6w .. 6w + 5 of each tile: key half
-    // kh = w / 4, 64-byte column groups 6 (w % 4) + t.  Lane i of a K chunk
-    // fetches row 16kh + i % 16 at byte 16 (i / 16) of the group; lane i of a V
-    // chunk row 16kh + (i % 32) / 2 at byte 32 (i / 32) + 16 (i % 2).  Rows past
-    // the key range re-read the range's last row (their scores are masked to
-    // -inf, their weights are 0).  Phases past the end re-read the last phase
-    // of the same kind into the ring slot of phase ph - 3, whose readers are
-    // done, so every tile issues the same way; the DMA is drained after the
-    // loop.  The DMA is untracked (dma16_untracked): the phase waits order it.
-    const int dkh = w / NA, dcol = 64 * CPW * (w % NA);
-    const int rowK = 16 * dkh + (lane & 15), colK = dcol + 16 * (lane >> 4);
-    const int rowV = 16 * dkh + ((lane & 31) >> 1), colV = dcol + 32 * (lane >> 5) + 16 * (lane & 1);
+    // The key window of tile t starts at row n0 - lo(t): a partial last tile
+    // is shifted back to end at the range's last key (its first lo rows
+    // repeat keys of the previous tile and are masked), so no DMA lane ever
+    // reads past the range.  A range shorter than a tile has one tile whose
+    // rows past the range re-read its last row instead (clamped below).
+    auto row_lo = [&](int tile) { return (tile == ntiles - 1 && nk >= BN) ? BN - (nk - tile * BN) : 0; };
+
+    // DMA.  Chunk m of a tile covers LDS bytes [1024 m, 1024 m + 1024): lane i
+    // lands on 16-byte slot u = 64 m + i, row u / 98, piece u % 98 (pieces 96
+    // and 97 are padding, which re-read piece 95).  Wavefront w issues chunks
+    // 6w .. 6w + 5, and wavefront 0 also chunk 48.  The per-lane source
+    // offsets are the same for every tile; the DMA is untracked
+    // (dma16_untracked): the waits in the tile loop order it.  Requests past
+    // the last tile re-read the last tile into a slot nobody reads any more,
+    // so every tile issues the same way; the DMA is drained after the loop.
+    unsigned doff[CPW + 1];
+#pragma unroll
+    for (int t = 0; t <= CPW; ++t) {
+        const int u = 64 * (t < CPW ? CPW * w + t : CHUNKS - 1) + lane;
+        const int r = u / (LROW / 16), piece = min(u - r * (LROW / 16), ROWB / 16 - 1);
+        doff[t] = (unsigned)(min(r, nk - 1) * ROWB + 16 * piece);
+    }
     const unsigned lds0 = lds_u32(lds);
     struct Dma {
         const char* src;
-        unsigned voff, m0;
+        unsigned m0;
     };
-    auto dma_setup = [&](int ph) {
-        const bool isv = ph & 1;
-        const int pr = ph < nphase ? ph : ph - 2;
-        const int n0 = (pr >> 1) * BN;
-        const int last = nk - 1 - n0;  // last valid row of the tile
+    // LDS slots: K(t) always in slot 0; V(t) in slot 1 + t % 2; the score
+    // exchange of tile t in the other one (where V(t - 1) was).
+    auto dma_setup = [&](bool v, int tile) {
+        tile = min(tile, ntiles - 1);
         Dma d;
-        d.src = (isv ? Vb : Kb) + (size_t)n0 * ROWB;
-        d.voff = (unsigned)(min(isv ? rowV : rowK, last) * ROWB + (isv ? colV : colK));
-        d.m0 = lds0 + (unsigned)((ph % NBUF) * BUFB + 1024 * CPW * w);
+        d.src = uniform_ptr((v ? Vb : Kb) + (size_t)(tile * BN - row_lo(tile)) * ROWB);
+        d.m0 = lds0 + (unsigned)(v ? (1 + (tile & 1)) * BUFB : 0);
         return d;
     };
-    auto dma_chunk = [&](const Dma& d, int t) { dma16_untracked(d.src + 64 * t, d.voff, d.m0 + 1024 * t); };
-    auto issue = [&](int ph) {
-        const Dma d = dma_setup(ph);
+    auto dma_chunk = [&](const Dma& d, int t) {
+        dma16_untracked(d.src, doff[t], d.m0 + 1024 * (CPW * w + t));
+    };
+    auto dma_last = [&](const Dma& d) {
+        if (w == 0) dma16_untracked(d.src, doff[CPW], d.m0 + 1024 * (CHUNKS - 1));
+    };
+    auto issue = [&](bool v, int tile) {
+        const Dma d = dma_setup(v, tile);
 #pragma unroll
         for (int t = 0; t < CPW; ++t) dma_chunk(d, t);
+        dma_last(d);
     };
 
     // Q^T operand of latent block 2h + cl, k-step s:
@@ -243,7 +255,7 @@ void flash16_kernel(Params p) {
     // the full wait after the Q loads leaves no compiler-visible load pending,
     // so the compiler adds no waits inside the tile loop (where only untracked
     // DMA is in flight).
-    issue(0);
+    issue(false, 0);
     v8 qr[CBW][KS];
 #pragma unroll
     for (int cl = 0; cl < CBW; ++cl) {
@@ -254,11 +266,12 @@ void flash16_kernel(Params p) {
     }
     wait_vmcnt<0>();
 
-    // Per-lane LDS read bases within a tile buffer: the K fragments of this
-    // wavefront's column groups 6a .. 6a + 5, the V pieces of its column
-    // blocks 12a .. 12a + 11; fragments differ by immediate offsets.
-    const int kread = 1024 * CPW * a + 16 * lane;
-    const int vread = 512 * DB * a + 8 * lane;
+    // Per-lane LDS read bases within a tile buffer (fragments differ by
+    // immediate offsets): K row j at byte 2 (d0 + 8g) (k-step s adds 64 s, key
+    // half kh adds 16 rows); V row 4g + e at byte 2 (d0 + 4q) for lane
+    // 16g + 4e + q (column block t adds 32 t, key half 16 rows).
+    const int kread = LROW * j + 2 * (d0 + 8 * g);
+    const int vread = LROW * (4 * g + (j >> 2)) + 2 * (d0 + 4 * (j & 3));
 
     if (tid == 0) restart_flag = 0;
 
@@ -272,8 +285,8 @@ void flash16_kernel(Params p) {
     f4 acc[CBW][DB];  // O^T[d0 + 16t + 4g + i][q0 + 16(2h + cl) + j]
 
     for (bool first = true;; first = false) {  // passes over the key range; a second is rare
-        if (!first) issue(0);
-        issue(1);
+        if (!first) issue(false, 0);
+        issue(true, 0);
 #pragma unroll
         for (int cl = 0; cl < CBW; ++cl)
 #pragma unroll
@@ -282,50 +295,50 @@ void flash16_kernel(Params p) {
         bool restart = false;
 
         for (int tile = 0; tile < ntiles; ++tile) {
-            const int n0 = tile * BN;
-            int ph = 2 * tile;
+            const int n0 = tile * BN, lo = row_lo(tile);
+            const unsigned vslot = (unsigned)((1 + (tile & 1)) * BUFB);
+            const unsigned xslot = (unsigned)((2 - (tile & 1)) * BUFB);
 
             // ---------------- partial scores over this wavefront's slice ----------------
+            // K(t) has landed (V(t) may still be in flight) for every
+            // wavefront, and every wavefront is done with V(t - 1), whose slot
+            // takes the exchange.
             wait_vmcnt<CPW>();
             lds_barrier();
-            char* kb = lds + (ph % NBUF) * BUFB;
             f4 sacc[2][CBW];
 #pragma unroll
             for (int kh = 0; kh < 2; ++kh)
 #pragma unroll
                 for (int cl = 0; cl < CBW; ++cl) sacc[kh][cl] = (f4){0.f, 0.f, 0.f, 0.f};
             {
-                // fragment f: k-step f >> 1, keys 16 (f & 1) .. +15
-                const lds_char* kr = opaque_lds(lds0 + (unsigned)((ph % NBUF) * BUFB + kread));
-                auto kfrag = [&](int f) { return *(const v8*)(kr + 1024 * ((f & 1) * 24 + (f >> 1))); };
-                const Dma dk = dma_setup(ph + 2);
-                // K fragments run KPF ahead of the MFMAs that use them; the
-                // phase-(ph + 2) DMA goes out one chunk per two fragments, so
-                // the address unit drains between issues.
+                // fragment f: k-step f >> 1, keys 16 (f & 1) .. +15; fragments
+                // run KPF ahead of the MFMAs that use them
+                const lds_char* kr = opaque_lds(lds0 + (unsigned)kread);
+                auto kfrag = [&](int f) { return *(const v8*)(kr + 16 * LROW * (f & 1) + 64 * (f >> 1)); };
                 v8 kf[2 * KS];
 #pragma unroll
                 for (int f = 0; f < KPF; ++f) kf[f] = kfrag(f);
 #pragma unroll
                 for (int f = 0; f < 2 * KS; ++f) {
                     if (f + KPF < 2 * KS) kf[f + KPF] = kfrag(f + KPF);
-                    if ((f & 1) == 0) dma_chunk(dk, f >> 1);
 #pragma unroll
                     for (int cl = 0; cl < CBW; ++cl)
                         sacc[f & 1][cl] = mfma32<T>(kf[f], qr[cl][f >> 1], sacc[f & 1][cl]);
                     __builtin_amdgcn_sched_barrier(0);
                 }
             }
-            // Every wavefront is done with K(t): its buffer carries the partial
-            // sums, slot (unit * 4 + slice), unit = block * 2 + key half,
-            // 64 lanes x 16 B each.
-            lds_barrier();
-            f4* xs = (f4*)kb;
+            // Partial sums, slot (unit * 4 + slice), unit = block * 2 + key
+            // half, 64 lanes x 16 B each, into the free slot.
+            f4* xs = (f4*)(lds + xslot);
 #pragma unroll
             for (int cl = 0; cl < CBW; ++cl)
 #pragma unroll
                 for (int kh = 0; kh < 2; ++kh)
                     xs[(((CBW * h + cl) * 2 + kh) * NA + a) * kWave + lane] = sacc[kh][cl];
+            // The partials are complete and every wavefront is done with K(t):
+            // request K(t + 1) into slot 0.
             lds_barrier();
+            issue(false, tile + 1);
             f4 sv = xs[(w * NA) * kWave + lane];
 #pragma unroll
             for (int src = 1; src < NA; ++src) sv += xs[(w * NA + src) * kWave + lane];
@@ -333,7 +346,10 @@ void flash16_kernel(Params p) {
             // ------ softmax weights of the owned unit (raw-dot units) ------
             float x[4];
 #pragma unroll
-            for (int i = 0; i < 4; ++i) x[i] = (n0 + 16 * kbo + 4 * g + i < nk) ? sv[i] : -INFINITY;
+            for (int i = 0; i < 4; ++i) {
+                const int r = 16 * kbo + 4 * g + i;  // tile row; its key is n0 - lo + r
+                x[i] = (r >= lo && n0 - lo + r < nk) ? sv[i] : -INFINITY;
+            }
             float tmax = fmaxf(fmaxf(x[0], x[1]), fmaxf(x[2], x[3]));
             tmax = wave_max16_groups(tmax);
             m_true = fmaxf(m_true, tmax);
@@ -360,7 +376,9 @@ void flash16_kernel(Params p) {
                 (u2v){pack2<T>(pw[0], pw[1]), pack2<T>(pw[2], pw[3])};
 
             // ---------------- O^T += V^T . P^T over this wavefront's slice ----------------
-            ph += 1;
+            // V(t) has landed (K(t + 1) may be in flight), P is complete, and
+            // every wavefront is done with the exchange slot, which takes
+            // V(t + 1).
             wait_vmcnt<CPW>();
             lds_barrier();
             // Every wavefront sets the flag (if at all) before this barrier, so
@@ -374,21 +392,22 @@ void flash16_kernel(Params p) {
             for (int cl = 0; cl < CBW; ++cl)
                 pt[cl] = __builtin_bit_cast(v8, pbuf[(CBW * h + cl) * kWave + lane]);
             {
-                lds_s4* vr = (lds_s4*)opaque_lds(lds0 + (unsigned)((ph % NBUF) * BUFB + vread));  // 64 per 512 B
-                const Dma dv = dma_setup(ph + 2);
+                lds_s4* vr = (lds_s4*)opaque_lds(lds0 + vslot + (unsigned)vread);  // 4 per 32 B
+                const Dma dv = dma_setup(true, tile + 1);
                 s4 va[DB], vc[DB];
 #pragma unroll
                 for (int t = 0; t < VPF; ++t) {
-                    va[t] = tr_read(vr + 64 * t);
-                    vc[t] = tr_read(vr + 64 * (48 + t));
+                    va[t] = tr_read(vr + 4 * t);
+                    vc[t] = tr_read(vr + 2 * LROW + 4 * t);
                 }
 #pragma unroll
                 for (int t = 0; t < DB; ++t) {
                     if (t + VPF < DB) {
-                        va[t + VPF] = tr_read(vr + 64 * (t + VPF));
-                        vc[t + VPF] = tr_read(vr + 64 * (48 + t + VPF));
+                        va[t + VPF] = tr_read(vr + 4 * (t + VPF));
+                        vc[t + VPF] = tr_read(vr + 2 * LROW + 4 * (t + VPF));
                     }
                     if ((t & 1) == 0) dma_chunk(dv, t >> 1);
+                    if (t == DB - 1) dma_last(dv);
                     const v8 vt = __builtin_bit_cast(
                         v8, __builtin_shufflevector(va[t], vc[t], 0, 1, 2, 3, 4, 5, 6, 7));
 #pragma unroll
@@ -398,8 +417,8 @@ void flash16_kernel(Params p) {
             }
         }
         if (!restart) break;
-        // Some latent's scores outgrew its reference: drain the DMA (phases up
-        // to ph + 2 may be in flight), clear the flag, and run the keys again
+        // Some latent's scores outgrew its reference: drain the DMA (K(t + 1)
+        // may be in flight), clear the flag, and run the keys again
         // with the reference raised to the max seen so far over both halves.
         wait_vmcnt<0>();
         lds_barrier();
