@@ -4,22 +4,29 @@
 // Contract (kernel_wmma.cu:42-137): Q arrives pre-scaled by 1/sqrt(D), so a
 // score is the plain dot product q.k.
 //
-// Work item = (batch, key split, 64 latents) on 8 wavefronts (two per SIMD);
-// tiles of 32 keys.  Wavefront w = (a, h), a = w & 3, h = w >> 2, owns the
-// 192-column slice a of D and the latent half h (two 16-latent blocks), for
-// the scores and for the output alike:
+// Work item = (batch, key split, 64 latents = four 16-latent blocks) on 8
+// wavefronts (two per SIMD); tiles of 32 keys.  Wavefront w has two roles:
 //
-//   partial S^T[32 keys x 32 q] = K[:, slice] . Q[half, slice]^T   2 x 2 x 6 MFMA
-//   O^T[slice x 32 q]         += V[:, slice]^T . P^T[half]         12 x 2 MFMA
+//   scores:  unit (block c = w / 2, key half k = w % 2):
+//            S^T[16 keys x 16 q] = K[16k.., :] . Q[block c, :]^T       24 MFMA
+//            over all of D, then the unit's softmax and its half of the
+//            block's P^T operand, in the wavefront's own registers;
+//   output:  column slice a = w % 4 (192 columns) of latent blocks
+//            2h, 2h + 1, h = w / 4:
+//            O^T[slice x 32 q] += V[:, slice]^T . P^T[blocks]          12 x 2 MFMA
 //
-// The four column slices' partial scores of a (latent block, 16-key half)
-// unit are summed through LDS (in the buffer the K tile just left); each of
-// the eight units has an owner wavefront that runs its softmax and writes its
-// half of the P operand.  The two owners of a latent block share the weights'
-// reference m_ref (exchanged on the first tile and at restarts); their running
-// maxima and sums are combined at the end.  Two wavefronts per SIMD double
-// the LDS read rate a single wavefront reaches, which bounds the MFMA
-// sections (the transposed V reads run at half the b128 rate).
+// so scores never cross wavefronts: the only exchange is the P operand (one
+// LDS write and read per block) plus, on the first tile and at restarts, the
+// weights' reference of a block's two owners.  Per tile, each SIMD issues 96
+// MFMAs; registers per lane: the Q block (96), the O^T accumulators (96).
+//
+// Softmax by passes: a row's weights are exp2(s - m_ref) with m_ref fixed for
+// a pass (the row max of the first tile, shared by the two owners of the
+// block); a pass restarts when some score exceeds m_ref by tau_log2<T> (in
+// exp2 units), which bounds every weight by 2^tau_log2<T> in the MFMA's input
+// type.  The exact running max is kept apart and folded in at the end, so
+// the normalised output and the split partials (pm = exact max) follow the
+// reference algorithm (kernel_wmma.cu:88-131, kernel_wmma_splitk.cu:80-139).
 //
 // Operand layouts.  In the S^T MFMA (A = K rows, B = Q^T) lane (j, g) ends
 // with S[q = j][4g + i], i < 4, of its 16-key half: four of the eight k-values
@@ -43,45 +50,39 @@
 // lanes read consecutive 16-byte pieces of a row (coalesced; the lanes that
 // land on padding re-read the row's last piece).  K and V tiles share one
 // pipeline: phases alternate QK(t) / PV(t), phase p reads buffer p % 3 and
-// requests phase p + 2; 3 buffers = 147 KiB.
+// requests phase p + 2 (into the buffer phase p - 1 just left); 3 buffers =
+// 147 KiB.  Two barriers per tile.
 #include "xattn_common.h"
 
 namespace xattn {
 namespace h16 {
 
 constexpr int BN = 32;                 // keys per tile
-constexpr int NA = 4;                  // column slices
-constexpr int NH = 2;                  // latent halves
-constexpr int NW = NA * NH;            // wavefronts per workgroup (8)
+constexpr int NA = 4;                  // output column slices
+constexpr int NW = 8;                  // wavefronts per workgroup
 constexpr int QB = 16;                 // latents per MFMA block
 constexpr int BM = 64;                 // latents per workgroup
 constexpr int NCB = BM / QB;           // latent blocks per workgroup (4)
-constexpr int CBW = NCB / NH;          // latent blocks per wavefront (2)
-constexpr int DW = kDim / NA;          // columns of D per wavefront (192)
-constexpr int KS = DW / 32;            // k-steps of a score MFMA chain (6)
+constexpr int CBW = 2;                 // latent blocks per wavefront in the output role
+constexpr int DW = kDim / NA;          // output columns per wavefront (192)
+constexpr int KSF = kDim / 32;         // k-steps of a full-D score chain (24)
 constexpr int DB = DW / 16;            // 16-column output blocks per wavefront (12)
 constexpr int ROWB = kDim * 2;         // bytes per K / V row in memory (1536)
 constexpr int LROW = ROWB + 32;        // bytes per tile row in LDS (1568)
 constexpr int BUFB = BN * LROW;        // bytes per tile buffer (49 KiB)
 constexpr int NBUF = 3;
-constexpr int CHUNKS = BUFB / 1024;        // 1 KiB DMA chunks per tile (49)
-constexpr int CPW = CHUNKS / NW;           // per wavefront (6); wavefront 0 also issues the last
-constexpr int NUNIT = NCB * 2;             // (latent block, key half) softmax units (8)
-constexpr int KPF = 4;                     // K fragments read ahead of their MFMAs
-constexpr int VPF = 3;                     // V column blocks read ahead of their MFMAs
+constexpr int CHUNKS = BUFB / 1024;    // 1 KiB DMA chunks per tile (49)
+constexpr int CPW = CHUNKS / NW;       // per wavefront (6); one wavefront also issues the last
+constexpr int KPF = 3;                 // K fragments read ahead of their MFMAs
+constexpr int VPF = 3;                 // V column blocks read ahead of their MFMAs
 
-static_assert(NUNIT == NW, "one softmax unit per wavefront");
+static_assert(NCB * 2 == NW && NA * 2 == NW, "one score unit and one output slice per wavefront");
+static_assert(CHUNKS * 1024 == BUFB && CHUNKS == CPW * NW + 1, "DMA split");
 static_assert(NBUF * BUFB + NCB * kWave * 16 + NW * QB * 8 + NCB * QB * 4 + 4 <= 160 * 1024,
               "LDS budget");
-static_assert(NUNIT * NA * kWave * 16 <= BUFB, "score exchange fits in a tile buffer");
-static_assert(CHUNKS * 1024 == BUFB && CHUNKS == CPW * NW + 1, "DMA split");
 
-// A row's weights are exp2(s - m_ref) with m_ref fixed for a whole pass over
-// the keys; a pass restarts when some score exceeds m_ref by tau_log2<T> (in
-// exp2 units), which bounds every weight by 2^tau_log2<T> in the MFMA's input
-// type: 2^15 for fp16 (largest finite 65504), 2^64 for bf16 (fp32's range).
 template <typename T> constexpr float tau_log2 = 64.0f;
-template <> constexpr float tau_log2<_Float16> = 15.0f;
+template <> constexpr float tau_log2<_Float16> = 15.0f;  // fp16's largest finite is 65504
 
 struct Params {
     const u16* Q;
@@ -97,7 +98,6 @@ struct Params {
 typedef unsigned int u4v __attribute__((ext_vector_type(4)));
 typedef unsigned int u2v __attribute__((ext_vector_type(2)));
 typedef short s4 __attribute__((ext_vector_type(4)));
-typedef short s8v __attribute__((ext_vector_type(8)));
 
 // Operand vector type of the MFMA for element type T (8 x 16-bit).
 template <typename T> struct Vec8;
@@ -152,12 +152,12 @@ void flash16_kernel(Params p) {
 
     const int tid = threadIdx.x;
     const int w = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63;
-    const int a = w & (NA - 1), h = w / NA;      // column slice, latent half
     const int j = lane & 15, g = lane >> 4;
     const int q0 = rb * BM;                     // first latent of the workgroup
-    const int d0 = a * DW;                      // first column of this wavefront's slice
-    const int cbo = w >> 1, kbo = w & 1;        // the softmax unit this wavefront owns
+    const int cbo = w >> 1, kbo = w & 1;        // score unit: latent block, key half
     const int qo = q0 + QB * cbo + j;           // ... and the latent of lane (j, *) in it
+    const int a = w % NA, h = w / NA;           // output role: column slice, latent half
+    const int d0 = a * DW;                      // first column of the slice
 
     int k0 = 0, k1 = p.NI;
     if (PARTIAL) {
@@ -199,6 +199,7 @@ void flash16_kernel(Params p) {
     __builtin_assume(nk >= 1);
     const int ntiles = (nk + BN - 1) / BN;
     __builtin_assume(ntiles >= 1);
+    const int nphase = 2 * ntiles;
 
     // The key window of tile t starts at row n0 - lo(t): a partial last tile
     // is shifted back to end at the range's last key (its first lo rows
@@ -212,13 +213,14 @@ void flash16_kernel(Params p) {
     // and 97 are padding, which re-read piece 95).  Wavefront w issues chunks
     // 6w .. 6w + 5, and wavefront 0 also chunk 48.  The per-lane source
     // offsets are the same for every tile; the DMA is untracked
-    // (dma16_untracked): the waits in the tile loop order it.  Requests past
-    // the last tile re-read the last tile into a slot nobody reads any more,
-    // so every tile issues the same way; the DMA is drained after the loop.
+    // (dma16_untracked): the phase waits order it.  Phases past the end re-read
+    // the last phase of the same kind into the buffer of phase ph - 3, whose
+    // readers are done, so every tile issues the same way; the DMA is drained
+    // after the loop.
     unsigned doff[CPW + 1];
 #pragma unroll
     for (int t = 0; t <= CPW; ++t) {
-        const int u = 64 * (t < CPW ? CPW * w + t : CHUNKS - 1) + lane;
+        const int u = 64 * (t < CPW ? CPW * w + t : CHUNKS - 1) + lane;  // t = CPW: chunk 48
         const int r = u / (LROW / 16), piece = min(u - r * (LROW / 16), ROWB / 16 - 1);
         doff[t] = (unsigned)(min(r, nk - 1) * ROWB + 16 * piece);
     }
@@ -227,13 +229,12 @@ void flash16_kernel(Params p) {
         const char* src;
         unsigned m0;
     };
-    // LDS slots: K(t) always in slot 0; V(t) in slot 1 + t % 2; the score
-    // exchange of tile t in the other one (where V(t - 1) was).
-    auto dma_setup = [&](bool v, int tile) {
-        tile = min(tile, ntiles - 1);
+    auto dma_setup = [&](int ph) {
+        const int pr = ph < nphase ? ph : ph - 2;
+        const int tile = pr >> 1;
         Dma d;
-        d.src = uniform_ptr((v ? Vb : Kb) + (size_t)(tile * BN - row_lo(tile)) * ROWB);
-        d.m0 = lds0 + (unsigned)(v ? (1 + (tile & 1)) * BUFB : 0);
+        d.src = uniform_ptr(((ph & 1) ? Vb : Kb) + (size_t)(tile * BN - row_lo(tile)) * ROWB);
+        d.m0 = lds0 + (unsigned)((ph % NBUF) * BUFB);
         return d;
     };
     auto dma_chunk = [&](const Dma& d, int t) {
@@ -242,35 +243,34 @@ void flash16_kernel(Params p) {
     auto dma_last = [&](const Dma& d) {
         if (w == 0) dma16_untracked(d.src, doff[CPW], d.m0 + 1024 * (CHUNKS - 1));
     };
-    auto issue = [&](bool v, int tile) {
-        const Dma d = dma_setup(v, tile);
+    auto issue = [&](int ph) {
+        const Dma d = dma_setup(ph);
 #pragma unroll
         for (int t = 0; t < CPW; ++t) dma_chunk(d, t);
         dma_last(d);
     };
 
-    // Q^T operand of latent block 2h + cl, k-step s:
-    // Q[q0 + 16(2h + cl) + j][d0 + 32s + 8g .. +7] (48 registers).  Latents past
-    // NL repeat the last one; they are not stored.  K(0) is requested first;
-    // the full wait after the Q loads leaves no compiler-visible load pending,
-    // so the compiler adds no waits inside the tile loop (where only untracked
+    // Q^T operand of the score unit's block, k-step s:
+    // Q[q0 + 16 cbo + j][32s + 8g .. +7] (96 registers).  Latents past NL
+    // repeat the last one; they are not stored.  K(0) is requested first; the
+    // full wait after the Q loads leaves no compiler-visible load pending, so
+    // the compiler adds no waits inside the tile loop (where only untracked
     // DMA is in flight).
-    issue(false, 0);
-    v8 qr[CBW][KS];
+    issue(0);
+    v8 qr[KSF];
+    {
+        const int qc = min(qo, p.NL - 1);
+        const u16* qrow = p.Q + ((size_t)b * p.NL + qc) * kDim + 8 * g;
 #pragma unroll
-    for (int cl = 0; cl < CBW; ++cl) {
-        const int qc = min(q0 + QB * (CBW * h + cl) + j, p.NL - 1);
-        const u16* qrow = p.Q + ((size_t)b * p.NL + qc) * kDim + d0 + 8 * g;
-#pragma unroll
-        for (int s = 0; s < KS; ++s) qr[cl][s] = *(const v8*)(qrow + 32 * s);
+        for (int s = 0; s < KSF; ++s) qr[s] = *(const v8*)(qrow + 32 * s);
     }
     wait_vmcnt<0>();
 
     // Per-lane LDS read bases within a tile buffer (fragments differ by
-    // immediate offsets): K row j at byte 2 (d0 + 8g) (k-step s adds 64 s, key
-    // half kh adds 16 rows); V row 4g + e at byte 2 (d0 + 4q) for lane
-    // 16g + 4e + q (column block t adds 32 t, key half 16 rows).
-    const int kread = LROW * j + 2 * (d0 + 8 * g);
+    // immediate offsets): K row 16 kbo + j at byte 16 g (k-step s adds 64 s);
+    // V row 4g + e at byte 2 (d0 + 4q) for lane 16g + 4e + q (column block t
+    // adds 32 t, key half 16 rows).
+    const int kread = LROW * (16 * kbo + j) + 16 * g;
     const int vread = LROW * (4 * g + (j >> 2)) + 2 * (d0 + 4 * (j & 3));
 
     if (tid == 0) restart_flag = 0;
@@ -285,8 +285,8 @@ void flash16_kernel(Params p) {
     f4 acc[CBW][DB];  // O^T[d0 + 16t + 4g + i][q0 + 16(2h + cl) + j]
 
     for (bool first = true;; first = false) {  // passes over the key range; a second is rare
-        if (!first) issue(false, 0);
-        issue(true, 0);
+        if (!first) issue(0);
+        issue(1);
 #pragma unroll
         for (int cl = 0; cl < CBW; ++cl)
 #pragma unroll
@@ -296,52 +296,30 @@ void flash16_kernel(Params p) {
 
         for (int tile = 0; tile < ntiles; ++tile) {
             const int n0 = tile * BN, lo = row_lo(tile);
-            const unsigned vslot = (unsigned)((1 + (tile & 1)) * BUFB);
-            const unsigned xslot = (unsigned)((2 - (tile & 1)) * BUFB);
+            int ph = 2 * tile;
 
-            // ---------------- partial scores over this wavefront's slice ----------------
-            // K(t) has landed (V(t) may still be in flight) for every
-            // wavefront, and every wavefront is done with V(t - 1), whose slot
-            // takes the exchange.
+            // ---------------- scores of the owned unit over all of D ----------------
+            // K(t) has landed for every wavefront, and every wavefront is done
+            // with V(t - 1), whose buffer takes K(t + 1).
             wait_vmcnt<CPW>();
             lds_barrier();
-            f4 sacc[2][CBW];
-#pragma unroll
-            for (int kh = 0; kh < 2; ++kh)
-#pragma unroll
-                for (int cl = 0; cl < CBW; ++cl) sacc[kh][cl] = (f4){0.f, 0.f, 0.f, 0.f};
+            f4 sacc[2] = {(f4){0.f, 0.f, 0.f, 0.f}, (f4){0.f, 0.f, 0.f, 0.f}};
             {
-                // fragment f: k-step f >> 1, keys 16 (f & 1) .. +15; fragments
-                // run KPF ahead of the MFMAs that use them
-                const lds_char* kr = opaque_lds(lds0 + (unsigned)kread);
-                auto kfrag = [&](int f) { return *(const v8*)(kr + 16 * LROW * (f & 1) + 64 * (f >> 1)); };
-                v8 kf[2 * KS];
+                const lds_char* kr = opaque_lds(lds0 + (unsigned)((ph % NBUF) * BUFB + kread));
+                const Dma dk = dma_setup(ph + 2);
+                v8 kf[KSF];
 #pragma unroll
-                for (int f = 0; f < KPF; ++f) kf[f] = kfrag(f);
+                for (int s = 0; s < KPF; ++s) kf[s] = *(const v8*)(kr + 64 * s);
 #pragma unroll
-                for (int f = 0; f < 2 * KS; ++f) {
-                    if (f + KPF < 2 * KS) kf[f + KPF] = kfrag(f + KPF);
-#pragma unroll
-                    for (int cl = 0; cl < CBW; ++cl)
-                        sacc[f & 1][cl] = mfma32<T>(kf[f], qr[cl][f >> 1], sacc[f & 1][cl]);
+                for (int s = 0; s < KSF; ++s) {
+                    if (s + KPF < KSF) kf[s + KPF] = *(const v8*)(kr + 64 * (s + KPF));
+                    if ((s & 3) == 1) dma_chunk(dk, s >> 2);  // chunks 0..5 at s = 1, 5, .., 21
+                    if (s == KSF - 1) dma_last(dk);
+                    sacc[s & 1] = mfma32<T>(kf[s], qr[s], sacc[s & 1]);
                     __builtin_amdgcn_sched_barrier(0);
                 }
             }
-            // Partial sums, slot (unit * 4 + slice), unit = block * 2 + key
-            // half, 64 lanes x 16 B each, into the free slot.
-            f4* xs = (f4*)(lds + xslot);
-#pragma unroll
-            for (int cl = 0; cl < CBW; ++cl)
-#pragma unroll
-                for (int kh = 0; kh < 2; ++kh)
-                    xs[(((CBW * h + cl) * 2 + kh) * NA + a) * kWave + lane] = sacc[kh][cl];
-            // The partials are complete and every wavefront is done with K(t):
-            // request K(t + 1) into slot 0.
-            lds_barrier();
-            issue(false, tile + 1);
-            f4 sv = xs[(w * NA) * kWave + lane];
-#pragma unroll
-            for (int src = 1; src < NA; ++src) sv += xs[(w * NA + src) * kWave + lane];
+            const f4 sv = sacc[0] + sacc[1];
 
             // ------ softmax weights of the owned unit (raw-dot units) ------
             float x[4];
@@ -376,9 +354,9 @@ void flash16_kernel(Params p) {
                 (u2v){pack2<T>(pw[0], pw[1]), pack2<T>(pw[2], pw[3])};
 
             // ---------------- O^T += V^T . P^T over this wavefront's slice ----------------
-            // V(t) has landed (K(t + 1) may be in flight), P is complete, and
-            // every wavefront is done with the exchange slot, which takes
-            // V(t + 1).
+            // V(t) has landed, P is complete, and every wavefront is done with
+            // K(t), whose buffer takes V(t + 1).
+            ph += 1;
             wait_vmcnt<CPW>();
             lds_barrier();
             // Every wavefront sets the flag (if at all) before this barrier, so
@@ -392,8 +370,8 @@ void flash16_kernel(Params p) {
             for (int cl = 0; cl < CBW; ++cl)
                 pt[cl] = __builtin_bit_cast(v8, pbuf[(CBW * h + cl) * kWave + lane]);
             {
-                lds_s4* vr = (lds_s4*)opaque_lds(lds0 + vslot + (unsigned)vread);  // 4 per 32 B
-                const Dma dv = dma_setup(true, tile + 1);
+                lds_s4* vr = (lds_s4*)opaque_lds(lds0 + (unsigned)((ph % NBUF) * BUFB + vread));  // 4 per 32 B
+                const Dma dv = dma_setup(ph + 2);
                 s4 va[DB], vc[DB];
 #pragma unroll
                 for (int t = 0; t < VPF; ++t) {
@@ -417,9 +395,9 @@ void flash16_kernel(Params p) {
             }
         }
         if (!restart) break;
-        // Some latent's scores outgrew its reference: drain the DMA (K(t + 1)
-        // may be in flight), clear the flag, and run the keys again
-        // with the reference raised to the max seen so far over both halves.
+        // Some latent's scores outgrew its reference: drain the DMA (V(t + 1)
+        // may be in flight), clear the flag, and run the keys again with the
+        // reference raised to the max seen so far over both halves.
         wait_vmcnt<0>();
         lds_barrier();
         if (tid == 0) restart_flag = 0;
@@ -432,9 +410,9 @@ void flash16_kernel(Params p) {
 
     // Combine the two key halves of each latent (max and sum, both against
     // the shared m_ref), then normalise (or, for a partial, rescale to the
-    // exact max).
-    // A wavefront's m_ref is that of the latent block it owns a unit of; the
-    // output blocks it accumulates are weighted by their own blocks' m_ref.
+    // exact max).  A wavefront's m_ref is that of the block of its score
+    // unit; the output blocks it accumulates are weighted by their own
+    // blocks' m_ref.
     if (g == 0) stats[w * QB + j] = make_float2(m_true, lsum);
     if (g == 0 && kbo == 0) sref[cbo * QB + j] = m_ref;
     lds_barrier();
