@@ -21,8 +21,13 @@
 // K and V tiles are shared by the 4 wavefronts through LDS and arrive by
 // global->LDS DMA (16 B per lane, 1 KiB per wave instruction).  Phases
 // alternate QK(t), PV(t); phase p reads buffer p % 3, and the data of phase
-// p + 2 is requested at the start of phase p, so every tile has two phases
-// (~12k cycles) to arrive.  One barrier per phase.
+// p + 2 is requested during phase p, one chunk per 16 MFMAs (a burst of 48
+// chunks per CU at the start of a phase stalls every wavefront on the full
+// DMA queue), so every tile has about two phases (~12k cycles) to arrive.
+// Phases past the end re-read the last phase of the same kind into the
+// buffer of phase p - 1, whose readers are done, so the loop issues the same
+// way on every tile; the DMA is drained after the loop.  One barrier per
+// phase.
 //
 // Softmax in raw dot-product units by passes: a row's weights are
 // exp2((s - m_ref) c2) with m_ref fixed for the whole pass (the row max of
@@ -126,38 +131,31 @@ void flash_f32_kernel(Params p) {
     const int nphase = 2 * ntiles;
 
     // Phase ph (even: K of tile ph/2, odd: V of tile ph/2) -> buffer ph % 3.
+    // Wavefront w's chunks cover tile rows r0 .. r0 + 3, three 1 KiB chunks
+    // per row; chunk t of the phase is rows r0 + t / 3, floats 256 (t % 3)...
     // Rows past k1 re-read row k1-1; their scores are masked to -inf and
-    // their weights are 0, so they only need to be finite.
+    // their weights are 0, so they only need to be finite.  The row is
+    // wave-uniform, so the clamp costs no vector instruction; the DMA is
+    // untracked (dma16_untracked), the phase waits below order it.
+    const unsigned lds0 = lds_u32(lds);
+    const int r0 = w * (CPW / ROW_CHUNKS);
+    const unsigned lane16 = 16u * lane;
+    auto dma_chunk = [&](int ph, int t) {
+        const int pr = ph < nphase ? ph : ph - 2;
+        const int r = t / ROW_CHUNKS, c = t % ROW_CHUNKS;
+        const int key = min(k0 + (pr >> 1) * BN + r0 + r, k1 - 1);
+        const float* src = uniform_ptr(((pr & 1) ? Vb : Kb) + (size_t)key * kDim + c * (kWave * 4));
+        dma16_untracked(src, lane16,
+                        lds0 + 4u * (unsigned)((ph % NBUF) * BUF + (r0 + r) * ROW + c * (kWave * 4)));
+    };
     auto issue = [&](int ph) {
-        const float* src = (ph & 1) ? Vb : Kb;
-        float* buf = lds + (ph % NBUF) * BUF;
-        const int n0 = k0 + (ph >> 1) * BN;
-        // this wave's chunks cover tile rows r0 .. r0 + CPW/3 - 1, 3 chunks each
-        const int r0 = w * (CPW / ROW_CHUNKS);
-        if (n0 + BN <= k1) {
-            // full tile: one wave-uniform base, compile-time chunk offsets,
-            // lane * 16 B the only per-lane part
-            const float* base = uniform_ptr(src + (size_t)(n0 + r0) * kDim);
 #pragma unroll
-            for (int t = 0; t < CPW; ++t) {
-                const int r = t / ROW_CHUNKS, c = t % ROW_CHUNKS;
-                dma16(base + r * kDim + c * (kWave * 4) + lane * 4,
-                      buf + (r0 + r) * ROW + c * (kWave * 4));
-            }
-        } else {
-            // last, partial tile: rows past k1 re-read row k1-1 (their scores
-            // are masked to -inf and their weights are 0)
-#pragma unroll
-            for (int t = 0; t < CPW; ++t) {
-                const int r = t / ROW_CHUNKS, c = t % ROW_CHUNKS;
-                const int key = min(n0 + r0 + r, k1 - 1);
-                dma16(uniform_ptr(src + (size_t)key * kDim + c * (kWave * 4)) + lane * 4,
-                      buf + (r0 + r) * ROW + c * (kWave * 4));
-            }
-        }
+        for (int t = 0; t < CPW; ++t) dma_chunk(ph, t);
     };
 
-    // Q^T operand, kept in registers for the whole key loop.
+    // Q^T operand, kept in registers for the whole key loop.  The wait after
+    // the loads leaves no compiler-visible load pending inside the loop.
+    issue(0);
     f4 qr[48];
     {
         const int qc = min(q0 + j, p.NL - 1);
@@ -165,7 +163,7 @@ void flash_f32_kernel(Params p) {
 #pragma unroll
         for (int u = 0; u < 48; ++u) qr[u] = *(const f4*)(qrow + 16 * u);
     }
-    issue(0);
+    wait_vmcnt<0>();
     issue(1);
 
     // The flag lives in the tile array: a second LDS object would give the
@@ -196,7 +194,6 @@ void flash_f32_kernel(Params p) {
             // ---------------- QK phase ----------------
             wait_vmcnt<CPW>();      // this phase landed; phase ph+1 may be in flight
             lds_barrier();
-            if (ph + 2 < nphase) issue(ph + 2);
             f4 s;
             {
                 // K operand reads run two 4-MFMA groups ahead; the sched_barrier
@@ -209,6 +206,7 @@ void flash_f32_kernel(Params p) {
 #pragma unroll
                 for (int u = 0; u < 48; ++u) {
                     if (u + 2 < 48) kv[(u + 2) % 3] = *(const f4*)(kb + 16 * (u + 2));
+                    if (u % 4 == 0) dma_chunk(ph + 2, u / 4);
                     const f4 k4 = kv[u % 3];
                     s0 = mfma4(k4[0], qr[u][0], s0);
                     s1 = mfma4(k4[1], qr[u][1], s1);
@@ -239,8 +237,7 @@ void flash_f32_kernel(Params p) {
 
             // ---------------- PV phase ----------------
             ph += 1;
-            if (ph + 1 < nphase) wait_vmcnt<CPW>();
-            else wait_vmcnt<0>();
+            wait_vmcnt<CPW>();
             lds_barrier();
             // Every wavefront sets the flag (if at all) before this barrier,
             // so all of them leave the pass at the same tile.
@@ -248,7 +245,6 @@ void flash_f32_kernel(Params p) {
                 restart = true;
                 break;
             }
-            if (ph + 2 < nphase) issue(ph + 2);
             {
                 // Group n = 12 r + T: V[4g + r][64T + 4j .. +3] feeds the four
                 // MFMAs of output tiles (T, c = 0..3) for k-slab r.
@@ -262,6 +258,7 @@ void flash_f32_kernel(Params p) {
                         const int rn = (n + 2) / 12, tn = (n + 2) % 12;
                         vv[(n + 2) % 3] = *(const f4*)(vb + rn * ROW + 64 * tn);
                     }
+                    if (n % 4 == 0) dma_chunk(ph + 2, n / 4);
                     const int r = n / 12, T = n % 12;
                     const f4 v4 = vv[n % 3];
 #pragma unroll
@@ -271,8 +268,8 @@ void flash_f32_kernel(Params p) {
             }
         }
         if (!restart) break;
-        // Some latent's scores outgrew its reference: drain the DMA (phases up
-        // to ph + 2 may be in flight), clear the flag, and run the keys again
+        // Some latent's scores outgrew its reference: drain the DMA (phase
+        // ph + 1 may be in flight), clear the flag, and run the keys again
         // with the reference raised to the max seen so far.
         wait_vmcnt<0>();
         lds_barrier();
@@ -280,6 +277,8 @@ void flash_f32_kernel(Params p) {
         m_ref = m_true;
         lds_barrier();
     }
+
+    wait_vmcnt<0>();  // the re-reads issued past the last phase
 
     // Fold the exact max back in: factor = exp(m_ref - m_true) <= 1.
     const float factor = fast_exp2((m_ref - m_true) * c2);
