@@ -140,11 +140,15 @@ void flash_f32_kernel(Params p) {
     const unsigned lds0 = lds_u32(lds);
     const int r0 = w * (CPW / ROW_CHUNKS);
     const unsigned lane16 = 16u * lane;
+    // K and V bases as scalar registers: the per-chunk offset is then scalar
+    // arithmetic, with no vector instruction between the MFMAs.
+    const float* const Ks = uniform_ptr(Kb);
+    const float* const Vs = uniform_ptr(Vb);
     auto dma_chunk = [&](int ph, int t) {
         const int pr = ph < nphase ? ph : ph - 2;
         const int r = t / ROW_CHUNKS, c = t % ROW_CHUNKS;
         const int key = min(k0 + (pr >> 1) * BN + r0 + r, k1 - 1);
-        const float* src = uniform_ptr(((pr & 1) ? Vb : Kb) + (size_t)key * kDim + c * (kWave * 4));
+        const float* src = ((pr & 1) ? Vs : Ks) + ((size_t)key * kDim + c * (kWave * 4));
         dma16_untracked(src, lane16,
                         lds0 + 4u * (unsigned)((ph % NBUF) * BUF + (r0 + r) * ROW + c * (kWave * 4)));
     };
