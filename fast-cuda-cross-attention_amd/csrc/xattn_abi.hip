@@ -186,6 +186,14 @@ int optimized_num_splits(int B, int NL, int NI, int cu) {
     return plan_splits(B, NL, NI, cu, 64, 16);
 }
 
+// Launch shape of the 16-bit entry points: 64-latent workgroups (8
+// wavefronts) when they fill the device; else 32-latent ones (4
+// wavefronts), split over the keys only if those do not fill it either.
+static void wmma_plan(int B, int NL, int NI, int cu, int* nw, int* S) {
+    *nw = (long long)B * h16_row_blocks(NL, 8) >= cu ? 8 : 4;
+    *S = plan_splits(B, NL, NI, cu, 8 * *nw, 32);
+}
+
 // Library-workspace split launch shared by the fp32 and 16-bit entry points.
 struct SplitScratch {
     float* po;
@@ -253,6 +261,14 @@ int xattn_plan_splits(int batch_size, int N_latent, int N_input, int cu_count,
     if (latents_per_workgroup < 1 || keys_per_tile < 1 || cu_count < 1) return 1;
     return plan_splits(batch_size, N_latent, N_input, cu_count, latents_per_workgroup,
                        keys_per_tile);
+}
+
+void xattn_wmma_plan(int batch_size, int N_latent, int N_input, int cu_count,
+                     int* latents_per_workgroup, int* num_splits) {
+    int nw = 8, S = 1;
+    wmma_plan(batch_size, N_latent, N_input, cu_count < 1 ? 1 : cu_count, &nw, &S);
+    if (latents_per_workgroup) *latents_per_workgroup = 8 * nw;
+    if (num_splits) *num_splits = S;
 }
 
 void launch_naive_kernel(const float* Q, const float* K, const float* V, float* output,
@@ -350,17 +366,18 @@ static void wmma_common(bool bf16, const char* who, const uint16_t* Q, const uin
     if (!validate_dim768(who, dim)) return;
     if (!validate_aligned16(who, Q, K, V, output, nullptr)) return;
     if (batch_size == 0 || N_latent == 0) return;
-    const int S = plan_splits(batch_size, N_latent, N_input, device_cu_count(), 64, 32);
+    int nw = 8, S = 1;
+    wmma_plan(batch_size, N_latent, N_input, device_cu_count(), &nw, &S);
     if (S <= 1) {
-        launch_flash16(bf16, Q, K, V, output, nullptr, nullptr, nullptr, batch_size, N_latent,
-                       N_input, 1, N_input, stream);
+        launch_flash16(bf16, nw, Q, K, V, output, nullptr, nullptr, nullptr, batch_size,
+                       N_latent, N_input, 1, N_input, stream);
         return;
     }
     const int tiles = (N_input + 31) / 32;
     const int chunk = ((tiles + S - 1) / S) * 32;
     SplitScratch sc;
     if (!split_scratch(&sc, batch_size, N_latent, S)) return;
-    if (!launch_flash16(bf16, Q, K, V, nullptr, sc.po, sc.pm, sc.pl, batch_size, N_latent,
+    if (!launch_flash16(bf16, nw, Q, K, V, nullptr, sc.po, sc.pm, sc.pl, batch_size, N_latent,
                         N_input, S, chunk, stream))
         return;
     launch_lse_combine(sc.po, sc.pm, sc.pl, output, batch_size * N_latent, S, stream);
@@ -382,7 +399,7 @@ static void wmma_splitk_common(bool bf16, const char* who, const uint16_t* Q, co
     // kernel_wmma_splitk.cu:52: chunk = ceil(NI / S) rounded up to a multiple of 16
     long long chunk = ((long long)N_input + num_splits - 1) / num_splits;
     chunk = (chunk + 15) / 16 * 16;
-    if (!launch_flash16(bf16, Q, K, V, nullptr, po, pm, pl, batch_size, N_latent, N_input,
+    if (!launch_flash16(bf16, 8, Q, K, V, nullptr, po, pm, pl, batch_size, N_latent, N_input,
                         num_splits, (int)chunk, stream))
         return;
     launch_lse_combine(po, pm, pl, output, batch_size * N_latent, num_splits, stream);

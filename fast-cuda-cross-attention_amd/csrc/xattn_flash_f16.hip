@@ -59,10 +59,7 @@ namespace h16 {
 
 constexpr int BN = 32;                 // keys per tile
 constexpr int NA = 4;                  // output column slices
-constexpr int NW = 8;                  // wavefronts per workgroup
 constexpr int QB = 16;                 // latents per MFMA block
-constexpr int BM = 64;                 // latents per workgroup
-constexpr int NCB = BM / QB;           // latent blocks per workgroup (4)
 constexpr int CBW = 2;                 // latent blocks per wavefront in the output role
 constexpr int DW = kDim / NA;          // output columns per wavefront (192)
 constexpr int KSF = kDim / 32;         // k-steps of a full-D score chain (24)
@@ -72,14 +69,26 @@ constexpr int LROW = ROWB + 32;        // bytes per tile row in LDS (1568)
 constexpr int BUFB = BN * LROW;        // bytes per tile buffer (49 KiB)
 constexpr int NBUF = 3;
 constexpr int CHUNKS = BUFB / 1024;    // 1 KiB DMA chunks per tile (49)
-constexpr int CPW = CHUNKS / NW;       // per wavefront (6); one wavefront also issues the last
-constexpr int KPF = 3;                 // K fragments read ahead of their MFMAs
-constexpr int VPF = 3;                 // V column blocks read ahead of their MFMAs
 
-static_assert(NCB * 2 == NW && NA * 2 == NW, "one score unit and one output slice per wavefront");
-static_assert(CHUNKS * 1024 == BUFB && CHUNKS == CPW * NW + 1, "DMA split");
-static_assert(NBUF * BUFB + NCB * kWave * 16 + NW * QB * 8 + NCB * QB * 4 + 4 <= 160 * 1024,
-              "LDS budget");
+// Workgroup shapes.  NW = 8: two wavefronts per SIMD, 64 latents; NW = 4: one
+// per SIMD, 32 latents (twice the workgroups for a given NL, for shapes whose
+// 64-latent blocks cannot fill the device: no key split, no merge pass).
+// Either way each wavefront owns one score unit and one output slice.
+template <int NW>
+struct Shape {
+    static constexpr int BM = 8 * NW;          // latents per workgroup
+    static constexpr int NCB = BM / QB;        // latent blocks (4 or 2)
+    static constexpr int CPW = CHUNKS / NW;    // DMA chunks per wavefront (6 or 12) ...
+    // ... and wavefront 0 also issues the last one
+    static constexpr int KPF = NW == 8 ? 3 : 4;  // K fragments read ahead of their MFMAs
+    static constexpr int VPF = NW == 8 ? 3 : 4;  // V column blocks read ahead of theirs
+    static constexpr int NCH = NW == 8 ? 2 : 4;  // score accumulator chains
+    static_assert(NCB * 2 == NW && (NW / NA) * CBW == NCB,
+                  "one score unit and one output slice per wavefront");
+    static_assert(CHUNKS * 1024 == BUFB && CHUNKS == CPW * NW + 1, "DMA split");
+    static_assert(NBUF * BUFB + NCB * kWave * 16 + NW * QB * 8 + NCB * QB * 4 + 4 <= 160 * 1024,
+                  "LDS budget");
+};
 
 template <typename T> constexpr float tau_log2 = 64.0f;
 template <> constexpr float tau_log2<_Float16> = 15.0f;  // fp16's largest finite is 65504
@@ -134,10 +143,12 @@ __device__ inline lds_char* opaque_lds(unsigned byte_addr) {
     return (lds_char*)byte_addr;
 }
 
-template <typename T, bool PARTIAL>
-__global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2)))
+template <typename T, bool PARTIAL, int NW>
+__global__ __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(NW / 4, NW / 4)))
 void flash16_kernel(Params p) {
     typedef typename Vec8<T>::type v8;
+    typedef Shape<NW> Sh;
+    constexpr int BM = Sh::BM, NCB = Sh::NCB, CPW = Sh::CPW, KPF = Sh::KPF, VPF = Sh::VPF;
     __shared__ __attribute__((aligned(16))) char lds[NBUF * BUFB];
     __shared__ __attribute__((aligned(16))) u4v pbuf[NCB * kWave];  // P^T operand per latent block
     __shared__ float2 stats[NW * QB];  // per owner and latent: (max, sum) or the reference
@@ -211,7 +222,7 @@ void flash16_kernel(Params p) {
     // DMA.  Chunk m of a tile covers LDS bytes [1024 m, 1024 m + 1024): lane i
     // lands on 16-byte slot u = 64 m + i, row u / 98, piece u % 98 (pieces 96
     // and 97 are padding, which re-read piece 95).  Wavefront w issues chunks
-    // 6w .. 6w + 5, and wavefront 0 also chunk 48.  The per-lane source
+    // CPW w .. CPW w + CPW - 1, and wavefront 0 also chunk 48.  The per-lane source
     // offsets are the same for every tile; the DMA is untracked
     // (dma16_untracked): the phase waits order it.  Phases past the end re-read
     // the last phase of the same kind into the buffer of phase ph - 3, whose
@@ -303,7 +314,9 @@ void flash16_kernel(Params p) {
             // with V(t - 1), whose buffer takes K(t + 1).
             wait_vmcnt<CPW>();
             lds_barrier();
-            f4 sacc[2] = {(f4){0.f, 0.f, 0.f, 0.f}, (f4){0.f, 0.f, 0.f, 0.f}};
+            f4 sacc[Sh::NCH];
+#pragma unroll
+            for (int c = 0; c < Sh::NCH; ++c) sacc[c] = (f4){0.f, 0.f, 0.f, 0.f};
             {
                 const lds_char* kr = opaque_lds(lds0 + (unsigned)((ph % NBUF) * BUFB + kread));
                 const Dma dk = dma_setup(ph + 2);
@@ -313,13 +326,16 @@ void flash16_kernel(Params p) {
 #pragma unroll
                 for (int s = 0; s < KSF; ++s) {
                     if (s + KPF < KSF) kf[s + KPF] = *(const v8*)(kr + 64 * (s + KPF));
-                    if ((s & 3) == 1) dma_chunk(dk, s >> 2);  // chunks 0..5 at s = 1, 5, .., 21
+                    constexpr int KSTEP = KSF / CPW;  // one chunk per KSTEP k-steps
+                    if (s % KSTEP == 1) dma_chunk(dk, s / KSTEP);
                     if (s == KSF - 1) dma_last(dk);
-                    sacc[s & 1] = mfma32<T>(kf[s], qr[s], sacc[s & 1]);
+                    sacc[s % Sh::NCH] = mfma32<T>(kf[s], qr[s], sacc[s % Sh::NCH]);
                     __builtin_amdgcn_sched_barrier(0);
                 }
             }
-            const f4 sv = sacc[0] + sacc[1];
+            f4 sv = sacc[0];
+#pragma unroll
+            for (int c = 1; c < Sh::NCH; ++c) sv += sacc[c];
 
             // ------ softmax weights of the owned unit (raw-dot units) ------
             float x[4];
@@ -384,7 +400,8 @@ void flash16_kernel(Params p) {
                         va[t + VPF] = tr_read(vr + 4 * (t + VPF));
                         vc[t + VPF] = tr_read(vr + 2 * LROW + 4 * (t + VPF));
                     }
-                    if ((t & 1) == 0) dma_chunk(dv, t >> 1);
+                    constexpr int VSTEP = DB / CPW;  // one chunk per VSTEP column blocks
+                    if (t % VSTEP == 0) dma_chunk(dv, t / VSTEP);
                     if (t == DB - 1) dma_last(dv);
                     const v8 vt = __builtin_bit_cast(
                         v8, __builtin_shufflevector(va[t], vc[t], 0, 1, 2, 3, 4, 5, 6, 7));
@@ -446,29 +463,41 @@ void flash16_kernel(Params p) {
 
 }  // namespace h16
 
-int h16_row_blocks(int NL) { return (NL + h16::BM - 1) / h16::BM; }
+int h16_row_blocks(int NL, int nw) { return (NL + 8 * nw - 1) / (8 * nw); }
 
-bool launch_flash16(bool bf16, const void* Q, const void* K, const void* V, float* out, float* po,
-                    float* pm, float* pl, int B, int NL, int NI, int S, int chunk,
+template <typename T, bool PARTIAL>
+static void launch16(int nw, dim3 grid, hipStream_t stream, const h16::Params& p) {
+    if (nw == 8)
+        hipLaunchKernelGGL((h16::flash16_kernel<T, PARTIAL, 8>), grid, dim3(8 * kWave), 0, stream, p);
+    else
+        hipLaunchKernelGGL((h16::flash16_kernel<T, PARTIAL, 4>), grid, dim3(4 * kWave), 0, stream, p);
+}
+
+bool launch_flash16(bool bf16, int nw, const void* Q, const void* K, const void* V, float* out,
+                    float* po, float* pm, float* pl, int B, int NL, int NI, int S, int chunk,
                     hipStream_t stream) {
+    if (nw != 4 && nw != 8) {
+        set_error(XATTN_ERR_INVALID_VALUE, "flash16: %d wavefronts per workgroup", nw);
+        return false;
+    }
     h16::Params p;
     p.Q = (const u16*)Q; p.K = (const u16*)K; p.V = (const u16*)V;
     p.out = out; p.po = po; p.pm = pm; p.pl = pl;
     p.B = B; p.NL = NL; p.NI = NI; p.S = S; p.chunk = chunk;
-    p.row_blocks = h16_row_blocks(NL);
+    p.row_blocks = h16_row_blocks(NL, nw);
     const long long nblk = (long long)B * p.row_blocks * S;
     if (nblk <= 0) return true;
     if (nblk > 0x7fffffffLL) {
         set_error(XATTN_ERR_INVALID_VALUE, "grid of %lld workgroups too large", nblk);
         return false;
     }
-    const dim3 grid((unsigned)nblk), block(h16::NW * kWave);
+    const dim3 grid((unsigned)nblk);
     if (bf16) {
-        if (po) hipLaunchKernelGGL((h16::flash16_kernel<__bf16, true>), grid, block, 0, stream, p);
-        else hipLaunchKernelGGL((h16::flash16_kernel<__bf16, false>), grid, block, 0, stream, p);
+        if (po) launch16<__bf16, true>(nw, grid, stream, p);
+        else launch16<__bf16, false>(nw, grid, stream, p);
     } else {
-        if (po) hipLaunchKernelGGL((h16::flash16_kernel<_Float16, true>), grid, block, 0, stream, p);
-        else hipLaunchKernelGGL((h16::flash16_kernel<_Float16, false>), grid, block, 0, stream, p);
+        if (po) launch16<_Float16, true>(nw, grid, stream, p);
+        else launch16<_Float16, false>(nw, grid, stream, p);
     }
     return check_launch(bf16 ? "flash_bf16" : "flash_f16");
 }

@@ -144,12 +144,25 @@ lib.xattn_optimized_num_splits.argtypes = [_I, _I, _I, _I]
 lib.xattn_optimized_num_splits.restype = ctypes.c_int
 lib.xattn_plan_splits.argtypes = [_I, _I, _I, _I, _I, _I]
 lib.xattn_plan_splits.restype = ctypes.c_int
+lib.xattn_wmma_plan.argtypes = [_I, _I, _I, _I, ctypes.POINTER(_I), ctypes.POINTER(_I)]
+lib.xattn_wmma_plan.restype = None
 
 # Workgroup shape of the MFMA kernels (csrc/xattn_flash_*.hip): 64 latents per
-# workgroup; 16-key tiles (fp32) and 32-key tiles (fp16/bf16).
+# workgroup (the 16-bit entry points drop to 32 when 64 cannot fill the
+# device, see wmma_plan); 16-key tiles (fp32) and 32-key tiles (fp16/bf16).
 LATENTS_PER_WORKGROUP = 64
 KEYS_PER_TILE_F32 = 16
 KEYS_PER_TILE_F16 = 32
+
+
+def wmma_plan(batch_size, N_latent, N_input, sm_count):
+    """(latents per workgroup, key splits) of launch_wmma_kernel and its bf16
+    twin: 64-latent workgroups when they fill ``sm_count`` compute units, else
+    32-latent ones, split over the keys only if those do not fill it."""
+    lpw, s = _I(0), _I(0)
+    lib.xattn_wmma_plan(batch_size, N_latent, N_input, int(sm_count), ctypes.byref(lpw),
+                        ctypes.byref(s))
+    return lpw.value, s.value
 
 
 def plan_num_splits(N_latent, N_input, batch_size, sm_count, keys_per_tile=KEYS_PER_TILE_F32):

@@ -8,7 +8,7 @@ the workgroups the implementation launches and how many CUs they can occupy.
 Workgroups per call: naive ceil(Nl/4)*B*12 (64-column blocks); warp and
 tiled ceil(Nl/4)*B; vectorized ceil(Nl/64)*B times the key splits it plans
 when that alone would leave CUs idle; splitk ceil(Nl/64)*B*S; the 16-bit
-entry points ceil(Nl/64)*B times their planned splits.  act_cu =
+entry points ceil(Nl/64 or Nl/32)*B times their planned splits (wmma_plan).  act_cu =
 min(workgroups, CUs) is the number of CUs that get any work.
 
     python experiments/bench_perceiver_nl.py
@@ -43,9 +43,12 @@ def workgroups(cw, impl, B, nl, ni, cu):
         return rows * cw.lib.xattn_optimized_num_splits(B, nl, ni, cu)
     if impl == "splitk":
         return rows * cw.plan_num_splits(nl, ni, B, cu)
-    if impl.startswith("wmma"):
+    if impl.startswith("wmma_splitk"):
         tile = cw.KEYS_PER_TILE_F16
         return rows * cw.lib.xattn_plan_splits(B, nl, ni, cu, cw.LATENTS_PER_WORKGROUP, tile)
+    if impl.startswith("wmma"):
+        lpw, s = cw.wmma_plan(B, nl, ni, cu)
+        return math.ceil(nl / lpw) * B * s
     return rows
 
 

@@ -144,11 +144,19 @@ int xattn_optimized_num_splits(int batch_size, int N_latent, int N_input,
                                int cu_count);
 /* Key splits that make batch_size * ceil(N_latent / latents_per_workgroup)
  * workgroups fill cu_count compute units once, each split a whole number of
- * keys_per_tile-key tiles.  Both MFMA kernels use 64 latents per workgroup;
- * tiles are 16 keys (fp32) and 32 keys (fp16/bf16).  Replaces the
+ * keys_per_tile-key tiles.  The fp32 kernel uses 64 latents per workgroup,
+ * the 16-bit one 64 or 32 (xattn_wmma_plan); tiles are 16 keys (fp32) and
+ * 32 keys (fp16/bf16).  Replaces the
  * block-count heuristic of cuda_wrappers.py:456-467 for these kernels. */
 int xattn_plan_splits(int batch_size, int N_latent, int N_input, int cu_count,
                       int latents_per_workgroup, int keys_per_tile);
+/* Launch shape launch_wmma_kernel / launch_wmma_bf16_kernel use (no
+ * reference counterpart): 64-latent workgroups when batch_size *
+ * ceil(N_latent / 64) fills cu_count compute units, else 32-latent ones,
+ * split over the keys (32-key tiles) only if those do not fill it either.
+ * Writes the latents per workgroup and the number of key splits. */
+void xattn_wmma_plan(int batch_size, int N_latent, int N_input, int cu_count,
+                     int* latents_per_workgroup, int* num_splits);
 
 #ifdef __cplusplus
 }

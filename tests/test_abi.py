@@ -69,6 +69,19 @@ def test_optimized_num_splits(cw):
         assert -(-tiles // chunk_tiles) == s  # tile-aligned chunks leave no empty split
 
 
+def test_wmma_plan(cw):
+    # (latents per workgroup, key splits) of launch_wmma_kernel on 256 CUs
+    assert cw.wmma_plan(32, 1024, 784, 256) == (64, 1)   # 512 x 64-latent blocks
+    assert cw.wmma_plan(16, 512, 784, 256) == (32, 1)    # 128 x 64 would not fill; 256 x 32 do
+    assert cw.wmma_plan(4, 1024, 784, 256) == (32, 2)    # 128 x 32 -> two 13/12-tile splits
+    assert cw.wmma_plan(1, 256, 4096, 256) == (32, 32)   # 8 blocks x 32 splits of 4 tiles
+    assert cw.wmma_plan(1, 64, 20, 256) == (32, 1)       # one tile: nothing to split
+    for b, nl, ni in [(1, 1, 1), (2, 100, 33), (3, 7, 5000), (64, 64, 784)]:
+        lpw, s = cw.wmma_plan(b, nl, ni, 256)
+        assert lpw in (32, 64) and 1 <= s <= -(-ni // 32)
+        assert s == cw.lib.xattn_plan_splits(b, nl, ni, 256, lpw, 32)
+
+
 def test_choose_num_splits_known_values(cw):
     # values worked out by hand from cuda_wrappers.py:456-467
     assert cw.choose_num_splits(256, 4096, 1) == 8            # sm 142, lpb 4
