@@ -6,6 +6,7 @@
 #include <stdio.h>
 #include <string.h>
 
+#include <algorithm>
 #include <mutex>
 
 #include "xattn_common.h"
@@ -182,8 +183,75 @@ int plan_splits(int B, int NL, int NI, int cu, int bm, int tile) {
     return (tiles + chunk_tiles - 1) / chunk_tiles;
 }
 
+// Modelled time (µs) of one fp32 launch with ds wavefronts per 16-latent
+// block (64/ds-latent workgroups) and S key splits of ct 16-key tiles each.
+// Fitted to launches on MI355X (256 CUs; 3 % mean error over B = 1..32,
+// N_latent = 64..1024, N_input = 784..50176): a 16-key tile costs a
+// workgroup 5.90 µs at 64 latents, 3.26 at 32 and 2.12 at 16 (smaller
+// workgroups stream more K/V from L2 and run the softmax more often per
+// FLOP), plus 0.39 µs per round of workgroups; a split launch adds the LSE
+// merge, 2.93 µs + 0.42 µs per MB of partials written and read back, + 0.07
+// µs per split while there are fewer merge rows (B * N_latent) than CUs.
+static double f32_cost(int B, int NL, int cu, int ds, long long S, long long ct) {
+    const double tile_us = ds == 1 ? 5.904 : ds == 2 ? 3.255 : 2.122;
+    const long long W = (long long)B * f32_row_blocks(NL, ds) * S;
+    const long long rounds = (W + cu - 1) / cu;
+    double t = (double)rounds * ((double)ct * tile_us + 0.39);
+    if (S > 1) {
+        const double rows = (double)B * NL;
+        t += 2.927 + 0.424 * rows * (double)S * (kDim * 4) * 1e-6 +
+             0.07 * (double)S * std::max(0.0, 1.0 - rows / cu);
+    }
+    return t;
+}
+
+// Wavefronts per 16-latent block (1, 2 or 4) for a launch of S key splits of
+// `chunk` keys each: the cheapest by f32_cost.
+static int f32_parts(int B, int NL, int NI, int S, int chunk, int cu) {
+    const long long ct = NI > 0 ? ((long long)std::min(chunk, NI) + 15) / 16 : 0;
+    int best = 1;
+    double best_t = 0.0;
+    for (int ds = 1; ds <= 4; ds *= 2) {
+        const double t = f32_cost(B, NL, cu, ds, S, ct);
+        if (ds == 1 || t < best_t) best = ds, best_t = t;
+    }
+    return best;
+}
+
+// Launch shape of launch_optimized_kernel: the (ds, S) pair of least
+// f32_cost over ds in {1, 2, 4} and S up to min(tiles, cu), with every split
+// a whole number of tiles.  The last shape is cached per thread.
+static void f32_plan(int B, int NL, int NI, int cu, int* ds, int* S) {
+    thread_local int key[4] = {-1, -1, -1, -1}, val[2] = {1, 1};
+    if (key[0] == B && key[1] == NL && key[2] == NI && key[3] == cu) {
+        *ds = val[0];
+        *S = val[1];
+        return;
+    }
+    int bd = 1, bs = 1;
+    const long long tiles = NI > 0 ? ((long long)NI + 15) / 16 : 0;
+    if (B > 0 && NL > 0 && tiles > 0) {
+        double best_t = -1.0;
+        const long long smax = std::min<long long>(tiles, cu);
+        for (int d = 1; d <= 4; d *= 2) {
+            for (long long s = 1; s <= smax; ++s) {
+                const long long ct = (tiles + s - 1) / s;
+                if ((tiles + ct - 1) / ct != s) continue;  // same chunks as a smaller s
+                const double t = f32_cost(B, NL, cu, d, s, ct);
+                if (best_t < 0.0 || t < best_t) best_t = t, bd = d, bs = (int)s;
+            }
+        }
+    }
+    key[0] = B, key[1] = NL, key[2] = NI, key[3] = cu;
+    val[0] = bd, val[1] = bs;
+    *ds = bd;
+    *S = bs;
+}
+
 int optimized_num_splits(int B, int NL, int NI, int cu) {
-    return plan_splits(B, NL, NI, cu, 64, 16);
+    int ds = 1, S = 1;
+    f32_plan(B, NL, NI, cu, &ds, &S);
+    return S;
 }
 
 // Launch shape of the 16-bit entry points: 64-latent workgroups (8
@@ -263,6 +331,22 @@ int xattn_plan_splits(int batch_size, int N_latent, int N_input, int cu_count,
                        keys_per_tile);
 }
 
+void xattn_f32_plan(int batch_size, int N_latent, int N_input, int cu_count,
+                    int* latents_per_workgroup, int* num_splits) {
+    int ds = 1, S = 1;
+    f32_plan(batch_size, N_latent, N_input, cu_count < 1 ? 1 : cu_count, &ds, &S);
+    if (latents_per_workgroup) *latents_per_workgroup = 64 / ds;
+    if (num_splits) *num_splits = S;
+}
+
+int xattn_f32_split_latents(int batch_size, int N_latent, int N_input, int num_splits,
+                            int cu_count) {
+    if (batch_size < 1 || N_latent < 1 || num_splits < 1) return 64;
+    const int chunk = (int)(((long long)std::max(N_input, 0) + num_splits - 1) / num_splits);
+    return 64 / f32_parts(batch_size, N_latent, N_input, num_splits, chunk,
+                          cu_count < 1 ? 1 : cu_count);
+}
+
 void xattn_wmma_plan(int batch_size, int N_latent, int N_input, int cu_count,
                      int* latents_per_workgroup, int* num_splits) {
     int nw = 8, S = 1;
@@ -322,9 +406,10 @@ void launch_optimized_kernel(const float* Q, const float* K, const float* V, flo
     if (!validate_dim768(who, dim)) return;
     if (!validate_aligned16(who, Q, K, V, output, nullptr)) return;
     if (batch_size == 0 || N_latent == 0) return;
-    const int S = optimized_num_splits(batch_size, N_latent, N_input, device_cu_count());
+    int ds = 1, S = 1;
+    f32_plan(batch_size, N_latent, N_input, device_cu_count(), &ds, &S);
     if (S <= 1) {
-        launch_flash_f32(Q, K, V, output, nullptr, nullptr, nullptr, batch_size, N_latent,
+        launch_flash_f32(ds, Q, K, V, output, nullptr, nullptr, nullptr, batch_size, N_latent,
                          N_input, 1, N_input, stream);
         return;
     }
@@ -332,8 +417,8 @@ void launch_optimized_kernel(const float* Q, const float* K, const float* V, flo
     const int chunk = ((tiles + S - 1) / S) * 16;
     SplitScratch sc;
     if (!split_scratch(&sc, batch_size, N_latent, S)) return;
-    if (!launch_flash_f32(Q, K, V, nullptr, sc.po, sc.pm, sc.pl, batch_size, N_latent, N_input,
-                          S, chunk, stream))
+    if (!launch_flash_f32(ds, Q, K, V, nullptr, sc.po, sc.pm, sc.pl, batch_size, N_latent,
+                          N_input, S, chunk, stream))
         return;
     launch_lse_combine(sc.po, sc.pm, sc.pl, output, batch_size * N_latent, S, stream);
 }
@@ -353,7 +438,9 @@ void launch_splitk_kernel(const float* Q, const float* K, const float* V, float*
     }
     // kernel_splitk.cu:59: chunk = ceil(NI / S)
     const int chunk = (int)(((long long)N_input + num_splits - 1) / num_splits);
-    if (!launch_flash_f32(Q, K, V, nullptr, po, pm, pl, batch_size, N_latent, N_input,
+    const int ds = f32_parts(batch_size, N_latent, N_input, num_splits, chunk,
+                             device_cu_count());
+    if (!launch_flash_f32(ds, Q, K, V, nullptr, po, pm, pl, batch_size, N_latent, N_input,
                           num_splits, chunk, stream))
         return;
     launch_lse_combine(po, pm, pl, output, batch_size * N_latent, num_splits, stream);

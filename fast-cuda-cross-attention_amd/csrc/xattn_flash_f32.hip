@@ -76,11 +76,20 @@ __device__ inline f4 mfma4(float a, float b, f4 c) {
     return __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, c, 0, 0, 0);
 }
 
-template <bool PARTIAL>
+template <bool PARTIAL, int DS>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1)))
 void flash_f32_kernel(Params p) {
-    // tile buffers, then the restart flag (one LDS object)
-    __shared__ __attribute__((aligned(16))) float lds[NBUF * BUF + 4];
+    static_assert(DS == 1 || DS == 2 || DS == 4, "column parts per latent block");
+    constexpr int BMW = BM / DS;     // latents per workgroup
+    constexpr int NU = 48 / DS;      // 16-column K-operand groups per wavefront
+    constexpr int NT = 12 / DS;      // 64-column output tiles per wavefront
+    constexpr int DSTEP = NU / CPW;  // MFMA groups per DMA chunk
+    constexpr int XCH = DS > 1 ? NW * kWave * 4 : 0;  // partial-score exchange (floats)
+    static_assert(NU % CPW == 0, "DMA spread");
+    static_assert((NBUF * BUF + XCH + 4) * 4 <= 160 * 1024, "LDS budget");
+
+    // tile buffers, the score exchange, then the restart flag (one LDS object)
+    __shared__ __attribute__((aligned(16))) float lds[NBUF * BUF + XCH + 4];
 
     const int item = xcd_remap(blockIdx.x, gridDim.x);
     const int rb = item % p.row_blocks;
@@ -91,7 +100,9 @@ void flash_f32_kernel(Params p) {
     const int tid = threadIdx.x;
     const int w = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63;
     const int j = lane & 15, g = lane >> 4;
-    const int q0 = rb * BM + w * QW;
+    // Wavefront w: latent block w / DS, output columns [768 dp / DS, ...).
+    const int dp = w % DS;
+    const int q0 = rb * BMW + (w / DS) * QW;
 
     int k0 = 0, k1 = p.NI;
     if (PARTIAL) {
@@ -111,9 +122,9 @@ void flash_f32_kernel(Params p) {
                 ? p.po + (((size_t)b * p.NL + q) * p.S + split) * kDim
                 : p.out + ((size_t)b * p.NL + q) * kDim;
 #pragma unroll
-            for (int T = 0; T < 12; ++T) *(f4*)(dst + 64 * T + 4 * j) = z;
+            for (int T = 0; T < NT; ++T) *(f4*)(dst + 64 * (NT * dp + T) + 4 * j) = z;
         }
-        if (PARTIAL && g == 0 && q0 + j < p.NL) {
+        if (PARTIAL && dp == 0 && g == 0 && q0 + j < p.NL) {
             const size_t pi = ((size_t)b * p.NL + q0 + j) * p.S + split;
             p.pm[pi] = -FLT_MAX;
             p.pl[pi] = 0.f;
@@ -157,28 +168,52 @@ void flash_f32_kernel(Params p) {
         for (int t = 0; t < CPW; ++t) dma_chunk(ph, t);
     };
 
-    // Q^T operand, kept in registers for the whole key loop.  The wait after
-    // the loads leaves no compiler-visible load pending inside the loop.
+    // Q^T operand (this wavefront's columns), kept in registers for the whole
+    // key loop.  The wait after the loads leaves no compiler-visible load
+    // pending inside the loop.
     issue(0);
-    f4 qr[48];
+    f4 qr[NU];
     {
         const int qc = min(q0 + j, p.NL - 1);
-        const float* qrow = p.Q + ((size_t)b * p.NL + qc) * kDim + 4 * g;
+        const float* qrow = p.Q + ((size_t)b * p.NL + qc) * kDim + 4 * g + 16 * NU * dp;
 #pragma unroll
-        for (int u = 0; u < 48; ++u) qr[u] = *(const f4*)(qrow + 16 * u);
+        for (int u = 0; u < NU; ++u) qr[u] = *(const f4*)(qrow + 16 * u);
     }
     wait_vmcnt<0>();
     issue(1);
 
-    // The flag lives in the tile array: a second LDS object would give the
-    // LDS reads alias-scope metadata and make the compiler drain the DMA
-    // before each of them.
-    int* restart_flag = (int*)(lds + NBUF * BUF);
+    // The exchange and the flag live in the tile array: a second LDS object
+    // would give the LDS reads alias-scope metadata and make the compiler
+    // drain the DMA before each of them.
+    float* const xch = lds + NBUF * BUF;
+    int* restart_flag = (int*)(lds + NBUF * BUF + XCH);
     if (tid == 0) *restart_flag = 0;
     const float c2 = kLog2e / sqrtf((float)kDim);
     const float tau_raw = kTauLog2 / c2;
     float m_true = -FLT_MAX, m_ref = -FLT_MAX, lsum;
-    f4 acc[12][4];
+    f4 acc[NT][4];
+    float pw[4];
+
+    // Online softmax of one tile's scores s (lane (j, g): latent j, keys
+    // n0 + 4g + i) into the P operand pw; raises the restart flag when a
+    // score outgrows the pass's reference.
+    auto softmax = [&](f4 s, int n0) {
+        float x[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) x[i] = (n0 + 4 * g + i < k1) ? s[i] : -INFINITY;
+        float tmax = fmaxf(fmaxf(x[0], x[1]), fmaxf(x[2], x[3]));
+        tmax = wave_max16_groups(tmax);
+        m_true = fmaxf(m_true, tmax);
+        if (m_ref == -FLT_MAX) m_ref = tmax;
+        if (__any(tmax > m_ref + tau_raw) && lane == 0) *restart_flag = 1;
+        float rs = 0.f;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            pw[i] = fast_exp2((x[i] - m_ref) * c2);
+            rs += pw[i];
+        }
+        lsum += wave_sum16_groups(rs);
+    };
 
     for (bool first = true;; first = false) {  // passes over the keys; a second is rare
         if (!first) {
@@ -186,7 +221,7 @@ void flash_f32_kernel(Params p) {
             issue(1);
         }
 #pragma unroll
-        for (int T = 0; T < 12; ++T)
+        for (int T = 0; T < NT; ++T)
 #pragma unroll
             for (int c = 0; c < 4; ++c) acc[T][c] = (f4){0.f, 0.f, 0.f, 0.f};
         lsum = 0.f;
@@ -198,19 +233,27 @@ void flash_f32_kernel(Params p) {
             // ---------------- QK phase ----------------
             wait_vmcnt<CPW>();      // this phase landed; phase ph+1 may be in flight
             lds_barrier();
+            if constexpr (DS > 1) {
+                // The flag of the previous tile's softmax (set before this
+                // barrier by every wavefront that raises it).
+                if (tile > 0 && __builtin_amdgcn_readfirstlane(*restart_flag)) {
+                    restart = true;
+                    break;
+                }
+            }
             f4 s;
             {
                 // K operand reads run two 4-MFMA groups ahead; the sched_barrier
-                // keeps the scheduler from hoisting all 48 reads (192 VGPRs).
-                const float* kb = lds + (ph % NBUF) * BUF + j * ROW + 4 * g;
+                // keeps the scheduler from hoisting all of them.
+                const float* kb = lds + (ph % NBUF) * BUF + j * ROW + 4 * g + 16 * NU * dp;
                 f4 s0 = {0.f, 0.f, 0.f, 0.f}, s1 = s0;
                 f4 kv[3];
                 kv[0] = *(const f4*)(kb);
                 kv[1] = *(const f4*)(kb + 16);
 #pragma unroll
-                for (int u = 0; u < 48; ++u) {
-                    if (u + 2 < 48) kv[(u + 2) % 3] = *(const f4*)(kb + 16 * (u + 2));
-                    if (u % 4 == 0) dma_chunk(ph + 2, u / 4);
+                for (int u = 0; u < NU; ++u) {
+                    if (u + 2 < NU) kv[(u + 2) % 3] = *(const f4*)(kb + 16 * (u + 2));
+                    if (u % DSTEP == 0) dma_chunk(ph + 2, u / DSTEP);
                     const f4 k4 = kv[u % 3];
                     s0 = mfma4(k4[0], qr[u][0], s0);
                     s1 = mfma4(k4[1], qr[u][1], s1);
@@ -221,54 +264,61 @@ void flash_f32_kernel(Params p) {
                 s = s0 + s1;
             }
 
-            // ---------------- online softmax ----------------
-            float x[4];
-#pragma unroll
-            for (int i = 0; i < 4; ++i) x[i] = (n0 + 4 * g + i < k1) ? s[i] : -INFINITY;
-            float tmax = fmaxf(fmaxf(x[0], x[1]), fmaxf(x[2], x[3]));
-            tmax = wave_max16_groups(tmax);
-            m_true = fmaxf(m_true, tmax);
-            if (m_ref == -FLT_MAX) m_ref = tmax;
-            if (__any(tmax > m_ref + tau_raw) && lane == 0) *restart_flag = 1;
-            float pw[4];
-            float rs = 0.f;
-#pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                pw[i] = fast_exp2((x[i] - m_ref) * c2);
-                rs += pw[i];
+            if constexpr (DS == 1) {
+                softmax(s, n0);
+            } else {
+                // this wavefront's share of the block's scores, summed after
+                // the next barrier
+                *(f4*)(xch + (w * kWave + lane) * 4) = s;
             }
-            lsum += wave_sum16_groups(rs);
 
             // ---------------- PV phase ----------------
             ph += 1;
             wait_vmcnt<CPW>();
             lds_barrier();
-            // Every wavefront sets the flag (if at all) before this barrier,
-            // so all of them leave the pass at the same tile.
-            if (__builtin_amdgcn_readfirstlane(*restart_flag)) {
-                restart = true;
-                break;
+            if constexpr (DS == 1) {
+                // Every wavefront sets the flag (if at all) before this barrier,
+                // so all of them leave the pass at the same tile.
+                if (__builtin_amdgcn_readfirstlane(*restart_flag)) {
+                    restart = true;
+                    break;
+                }
+            } else {
+                // Every wavefront of the block sums the shares in the same
+                // order, so all of them hold bit-identical scores and weights.
+                const float* xs = xch + ((w - dp) * kWave + lane) * 4;
+                f4 st = *(const f4*)(xs);
+#pragma unroll
+                for (int d = 1; d < DS; ++d) st += *(const f4*)(xs + d * kWave * 4);
+                softmax(st, n0);
             }
             {
-                // Group n = 12 r + T: V[4g + r][64T + 4j .. +3] feeds the four
-                // MFMAs of output tiles (T, c = 0..3) for k-slab r.
-                const float* vb = lds + (ph % NBUF) * BUF + 4 * j + 4 * g * ROW;
+                // Group n = NT r + T: V[4g + r][64 (NT dp + T) + 4j .. +3] feeds
+                // the four MFMAs of output tiles (T, c = 0..3) for k-slab r.
+                const float* vb = lds + (ph % NBUF) * BUF + 4 * j + 4 * g * ROW + 64 * NT * dp;
                 f4 vv[3];
                 vv[0] = *(const f4*)(vb);
-                vv[1] = *(const f4*)(vb + 64);
+                vv[1] = *(const f4*)(vb + (1 / NT) * ROW + 64 * (1 % NT));
 #pragma unroll
-                for (int n = 0; n < 48; ++n) {
-                    if (n + 2 < 48) {
-                        const int rn = (n + 2) / 12, tn = (n + 2) % 12;
+                for (int n = 0; n < 4 * NT; ++n) {
+                    if (n + 2 < 4 * NT) {
+                        const int rn = (n + 2) / NT, tn = (n + 2) % NT;
                         vv[(n + 2) % 3] = *(const f4*)(vb + rn * ROW + 64 * tn);
                     }
-                    if (n % 4 == 0) dma_chunk(ph + 2, n / 4);
-                    const int r = n / 12, T = n % 12;
+                    if (n % DSTEP == 0) dma_chunk(ph + 2, n / DSTEP);
+                    const int r = n / NT, T = n % NT;
                     const f4 v4 = vv[n % 3];
 #pragma unroll
                     for (int c = 0; c < 4; ++c) acc[T][c] = mfma4(pw[r], v4[c], acc[T][c]);
                     __builtin_amdgcn_sched_barrier(0);
                 }
+            }
+        }
+        if constexpr (DS > 1) {
+            // the last tile's flag
+            if (!restart) {
+                lds_barrier();
+                restart = __builtin_amdgcn_readfirstlane(*restart_flag) != 0;
             }
         }
         if (!restart) break;
@@ -301,12 +351,12 @@ void flash_f32_kernel(Params p) {
             ? p.po + (((size_t)b * p.NL + q) * p.S + split) * kDim
             : p.out + ((size_t)b * p.NL + q) * kDim;
 #pragma unroll
-        for (int T = 0; T < 12; ++T) {
+        for (int T = 0; T < NT; ++T) {
             f4 o = {acc[T][0][i], acc[T][1][i], acc[T][2][i], acc[T][3][i]};
-            *(f4*)(dst + 64 * T + 4 * j) = o * rsc[i];
+            *(f4*)(dst + 64 * (NT * dp + T) + 4 * j) = o * rsc[i];
         }
     }
-    if (PARTIAL && g == 0 && q0 + j < p.NL) {
+    if (PARTIAL && dp == 0 && g == 0 && q0 + j < p.NL) {
         const size_t pi = ((size_t)b * p.NL + q0 + j) * p.S + split;
         p.pm[pi] = m_true / sqrtf((float)kDim);
         p.pl[pi] = lsum * factor;
@@ -368,27 +418,37 @@ void lse_combine_kernel(const float* __restrict__ po, const float* __restrict__ 
 // Host launch helpers (used by the C entry points in xattn_abi.hip)
 // --------------------------------------------------------------------------
 
-int f32_row_blocks(int NL) { return (NL + f32::BM - 1) / f32::BM; }
+int f32_row_blocks(int NL, int ds) { return (NL + f32::BM / ds - 1) / (f32::BM / ds); }
 
-bool launch_flash_f32(const float* Q, const float* K, const float* V, float* out,
+template <bool PARTIAL>
+static void launch_f32(int ds, unsigned nblk, hipStream_t stream, const f32::Params& p) {
+    if (ds == 4)
+        hipLaunchKernelGGL((f32::flash_f32_kernel<PARTIAL, 4>), dim3(nblk), dim3(256), 0, stream, p);
+    else if (ds == 2)
+        hipLaunchKernelGGL((f32::flash_f32_kernel<PARTIAL, 2>), dim3(nblk), dim3(256), 0, stream, p);
+    else
+        hipLaunchKernelGGL((f32::flash_f32_kernel<PARTIAL, 1>), dim3(nblk), dim3(256), 0, stream, p);
+}
+
+bool launch_flash_f32(int ds, const float* Q, const float* K, const float* V, float* out,
                       float* po, float* pm, float* pl, int B, int NL, int NI,
                       int S, int chunk, hipStream_t stream) {
+    if (ds != 1 && ds != 2 && ds != 4) {
+        set_error(XATTN_ERR_INVALID_VALUE, "flash_f32: column parts %d not in {1, 2, 4}", ds);
+        return false;
+    }
     f32::Params p;
     p.Q = Q; p.K = K; p.V = V; p.out = out; p.po = po; p.pm = pm; p.pl = pl;
     p.B = B; p.NL = NL; p.NI = NI; p.S = S; p.chunk = chunk;
-    p.row_blocks = f32_row_blocks(NL);
+    p.row_blocks = f32_row_blocks(NL, ds);
     const long long nblk = (long long)B * p.row_blocks * S;
     if (nblk <= 0) return true;
     if (nblk > 0x7fffffffLL) {
         set_error(XATTN_ERR_INVALID_VALUE, "grid of %lld workgroups too large", nblk);
         return false;
     }
-    if (po)
-        hipLaunchKernelGGL(f32::flash_f32_kernel<true>, dim3((unsigned)nblk), dim3(256), 0,
-                           stream, p);
-    else
-        hipLaunchKernelGGL(f32::flash_f32_kernel<false>, dim3((unsigned)nblk), dim3(256), 0,
-                           stream, p);
+    if (po) launch_f32<true>(ds, (unsigned)nblk, stream, p);
+    else launch_f32<false>(ds, (unsigned)nblk, stream, p);
     return check_launch("flash_f32");
 }
 

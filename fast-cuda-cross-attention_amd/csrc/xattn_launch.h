@@ -17,9 +17,10 @@ bool validate_splits(const char* who, const void* po, const void* pm, const void
 
 // fp32 MFMA flash kernel.  po == nullptr: normalised output over all keys
 // (S must be 1).  Otherwise: unnormalised split partials, split s covering
-// keys [s*chunk, min((s+1)*chunk, NI)).
-int f32_row_blocks(int NL);
-bool launch_flash_f32(const float* Q, const float* K, const float* V, float* out, float* po,
+// keys [s*chunk, min((s+1)*chunk, NI)).  ds = wavefronts per 16-latent block
+// (1, 2 or 4; each holds 768/ds columns of Q and O): 64/ds-latent workgroups.
+int f32_row_blocks(int NL, int ds);
+bool launch_flash_f32(int ds, const float* Q, const float* K, const float* V, float* out, float* po,
                       float* pm, float* pl, int B, int NL, int NI, int S, int chunk,
                       hipStream_t stream);
 bool launch_lse_combine(const float* po, const float* pm, const float* pl, float* out, int rows,

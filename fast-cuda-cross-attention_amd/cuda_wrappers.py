@@ -146,13 +146,29 @@ lib.xattn_plan_splits.argtypes = [_I, _I, _I, _I, _I, _I]
 lib.xattn_plan_splits.restype = ctypes.c_int
 lib.xattn_wmma_plan.argtypes = [_I, _I, _I, _I, ctypes.POINTER(_I), ctypes.POINTER(_I)]
 lib.xattn_wmma_plan.restype = None
+lib.xattn_f32_plan.argtypes = [_I, _I, _I, _I, ctypes.POINTER(_I), ctypes.POINTER(_I)]
+lib.xattn_f32_plan.restype = None
+lib.xattn_f32_split_latents.argtypes = [_I, _I, _I, _I, _I]
+lib.xattn_f32_split_latents.restype = ctypes.c_int
 
 # Workgroup shape of the MFMA kernels (csrc/xattn_flash_*.hip): 64 latents per
-# workgroup (the 16-bit entry points drop to 32 when 64 cannot fill the
-# device, see wmma_plan); 16-key tiles (fp32) and 32-key tiles (fp16/bf16).
+# workgroup (the fp32 entry points drop to 32 or 16, the 16-bit ones to 32,
+# when 64 cannot fill the device, see f32_plan and wmma_plan); 16-key tiles
+# (fp32) and 32-key tiles (fp16/bf16).
 LATENTS_PER_WORKGROUP = 64
 KEYS_PER_TILE_F32 = 16
 KEYS_PER_TILE_F16 = 32
+
+
+def f32_plan(batch_size, N_latent, N_input, sm_count):
+    """(latents per workgroup, key splits) of launch_optimized_kernel: 64, 32
+    or 16 latents per workgroup and whole-tile key splits, chosen by the
+    library's cost model (larger workgroups cost less per FLOP; smaller ones
+    and splits fill ``sm_count`` compute units at small batch * N_latent)."""
+    lpw, s = _I(0), _I(0)
+    lib.xattn_f32_plan(batch_size, N_latent, N_input, int(sm_count), ctypes.byref(lpw),
+                       ctypes.byref(s))
+    return lpw.value, s.value
 
 
 def wmma_plan(batch_size, N_latent, N_input, sm_count):
@@ -166,11 +182,16 @@ def wmma_plan(batch_size, N_latent, N_input, sm_count):
 
 
 def plan_num_splits(N_latent, N_input, batch_size, sm_count, keys_per_tile=KEYS_PER_TILE_F32):
-    """Default num_splits of the split-K drivers: enough key splits for the
-    64-latent workgroups to fill ``sm_count`` compute units once, each split a
-    whole number of tiles.  (The reference's ``choose_num_splits`` sizes for
-    4-latent blocks and 4x oversubscription; it is kept unchanged for callers
-    that use it directly.)"""
+    """Default num_splits of the split-K drivers, each split a whole number of
+    tiles: for fp32 (16-key tiles) the splits of f32_plan, whose workgroup
+    size launch_splitk_kernel then picks again; for the 16-bit split-K kernels
+    (32-key tiles) enough splits for 64-latent workgroups to fill
+    ``sm_count`` compute units once.  (The
+    reference's ``choose_num_splits`` sizes for 4-latent blocks and 4x
+    oversubscription; it is kept unchanged for callers that use it
+    directly.)"""
+    if keys_per_tile == KEYS_PER_TILE_F32:
+        return max(1, f32_plan(batch_size, N_latent, N_input, sm_count)[1])
     return max(1, lib.xattn_plan_splits(batch_size, N_latent, N_input, int(sm_count),
                                         LATENTS_PER_WORKGROUP, keys_per_tile))
 

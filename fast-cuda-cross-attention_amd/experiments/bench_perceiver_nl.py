@@ -40,9 +40,11 @@ def workgroups(cw, impl, B, nl, ni, cu):
         return math.ceil(nl / 4) * B * math.ceil(768 / 64)
     rows = math.ceil(nl / cw.LATENTS_PER_WORKGROUP) * B
     if impl == "vectorized":
-        return rows * cw.lib.xattn_optimized_num_splits(B, nl, ni, cu)
+        lpw, s = cw.f32_plan(B, nl, ni, cu)
+        return math.ceil(nl / lpw) * B * s
     if impl == "splitk":
-        return rows * cw.plan_num_splits(nl, ni, B, cu)
+        s = cw.plan_num_splits(nl, ni, B, cu)
+        return math.ceil(nl / cw.lib.xattn_f32_split_latents(B, nl, ni, s, cu)) * B * s
     if impl.startswith("wmma_splitk"):
         tile = cw.KEYS_PER_TILE_F16
         return rows * cw.lib.xattn_plan_splits(B, nl, ni, cu, cw.LATENTS_PER_WORKGROUP, tile)

@@ -144,12 +144,27 @@ int xattn_optimized_num_splits(int batch_size, int N_latent, int N_input,
                                int cu_count);
 /* Key splits that make batch_size * ceil(N_latent / latents_per_workgroup)
  * workgroups fill cu_count compute units once, each split a whole number of
- * keys_per_tile-key tiles.  The fp32 kernel uses 64 latents per workgroup,
- * the 16-bit one 64 or 32 (xattn_wmma_plan); tiles are 16 keys (fp32) and
+ * keys_per_tile-key tiles.  The fp32 kernel uses 64, 32 or 16 latents per
+ * workgroup (xattn_f32_plan), the 16-bit one 64 or 32 (xattn_wmma_plan);
+ * tiles are 16 keys (fp32) and
  * 32 keys (fp16/bf16).  Replaces the
  * block-count heuristic of cuda_wrappers.py:456-467 for these kernels. */
 int xattn_plan_splits(int batch_size, int N_latent, int N_input, int cu_count,
                       int latents_per_workgroup, int keys_per_tile);
+/* Launch shape launch_optimized_kernel uses (no reference counterpart):
+ * latents per workgroup (64, or 32 / 16 when two / four wavefronts share a
+ * 16-latent block, each holding 384 / 192 of the 768 columns) and key splits
+ * (16-key tiles, whole tiles per split), chosen by a cost model of the fp32
+ * kernel and the merge fitted to MI355X launches: larger workgroups cost
+ * less per FLOP, smaller ones and splits fill the device at small
+ * batch_size * N_latent, splits add the partials' round trip to memory. */
+void xattn_f32_plan(int batch_size, int N_latent, int N_input, int cu_count,
+                    int* latents_per_workgroup, int* num_splits);
+/* Latents per workgroup launch_splitk_kernel uses for num_splits key splits
+ * of ceil(N_input / num_splits) keys (64, 32 or 16, by the cost model of
+ * xattn_f32_plan; no reference counterpart). */
+int xattn_f32_split_latents(int batch_size, int N_latent, int N_input, int num_splits,
+                            int cu_count);
 /* Launch shape launch_wmma_kernel / launch_wmma_bf16_kernel use (no
  * reference counterpart): 64-latent workgroups when batch_size *
  * ceil(N_latent / 64) fills cu_count compute units, else 32-latent ones,

@@ -57,9 +57,9 @@ def test_xcd_remap_is_bijection(cw):
 def test_optimized_num_splits(cw):
     f = cw.lib.xattn_optimized_num_splits
     assert f(32, 1024, 784, 256) == 1      # 512 workgroups already fill 256 CUs
-    assert f(1, 64, 784, 256) == 49        # one workgroup: one 16-key tile per split
-    assert f(4, 1024, 784, 256) == 4
-    assert f(1, 256, 50176, 256) == 64
+    assert f(1, 64, 784, 256) == 25        # 4 x 16-latent blocks, two 16-key tiles per split
+    assert f(4, 1024, 784, 256) == 2       # 128 x 32-latent blocks x 2 splits
+    assert f(1, 256, 50176, 256) == 64     # 4 x 64-latent blocks x 64 splits of 49 tiles
     assert f(1, 64, 0, 256) == 1
     for b, nl, ni in [(1, 1, 1), (2, 100, 33), (1, 64, 17), (3, 7, 5000)]:
         s = f(b, nl, ni, 256)
@@ -67,6 +67,42 @@ def test_optimized_num_splits(cw):
         assert 1 <= s <= tiles
         chunk_tiles = -(-tiles // s)
         assert -(-tiles // chunk_tiles) == s  # tile-aligned chunks leave no empty split
+
+
+def test_f32_plan(cw):
+    # (latents per workgroup, key splits) of launch_optimized_kernel on 256
+    # CUs.  Each pair below is the fastest of the 3 workgroup sizes x 3-6
+    # split counts timed on an MI355X at that shape, except (1, 256, 16384),
+    # where the pick (32, 32) ran 1.5 % behind (64, 64).
+    assert cw.f32_plan(32, 1024, 784, 256) == (64, 1)    # 512 x 64-latent blocks
+    assert cw.f32_plan(16, 512, 784, 256) == (32, 1)     # 256 x 32-latent blocks: one round
+    assert cw.f32_plan(8, 1024, 784, 256) == (32, 1)
+    assert cw.f32_plan(12, 1024, 784, 256) == (32, 2)
+    assert cw.f32_plan(4, 1024, 784, 256) == (32, 2)
+    assert cw.f32_plan(1, 1024, 784, 256) == (32, 7)
+    assert cw.f32_plan(1, 256, 784, 256) == (16, 13)
+    assert cw.f32_plan(1, 64, 784, 256) == (16, 25)
+    assert cw.f32_plan(1, 256, 4096, 256) == (32, 32)
+    assert cw.f32_plan(1, 256, 16384, 256) == (32, 32)
+    assert cw.f32_plan(1, 256, 50176, 256) == (64, 64)
+    assert cw.f32_plan(1, 64, 0, 256) == (64, 1)
+    split = cw.lib.xattn_f32_split_latents
+    assert split(1, 256, 50176, 64, 256) == 64           # 4 x 64 splits fill the device
+    assert split(1, 256, 4096, 32, 256) == 32
+    assert split(1, 256, 4096, 16, 256) == 16
+    assert split(1, 1, 1, 1, 256) == 16                  # one tile: four wavefronts share it
+    for b, nl, ni in [(1, 1, 1), (2, 100, 33), (3, 7, 5000), (64, 64, 784), (5, 300, 784),
+                      (2, 70, 300), (1, 40, 200)]:
+        lpw, s = cw.f32_plan(b, nl, ni, 256)
+        tiles = -(-ni // 16)
+        assert lpw in (16, 32, 64) and 1 <= s <= tiles
+        assert s == cw.lib.xattn_optimized_num_splits(b, nl, ni, 256)
+        ct = -(-tiles // s)
+        assert -(-tiles // ct) == s  # whole-tile chunks leave no empty split
+        # launch_splitk_kernel with the planned splits and the same chunks
+        # picks the same workgroup size
+        if -(-(-(-ni // s)) // 16) == ct:
+            assert split(b, nl, ni, s, 256) == lpw
 
 
 def test_wmma_plan(cw):

@@ -146,11 +146,12 @@ def test_workgroup_counts(cw):
     cu = 256
     assert nl.workgroups(cw, "warp", 1, 16, 3136, cu) == 4
     assert nl.workgroups(cw, "naive", 2, 16, 3136, cu) == 2 * 4 * 12
-    # one 64-latent row block, split over the keys until the CUs are covered
-    s = cw.lib.xattn_optimized_num_splits(1, 64, 3136, cu)
-    assert s > 1 and nl.workgroups(cw, "vectorized", 1, 64, 3136, cu) == s
-    assert nl.workgroups(cw, "splitk", 1, 1024, 3136, cu) == 16 * cw.plan_num_splits(1024, 3136,
-                                                                                     1, cu)
+    # small row blocks, split over the keys until the CUs are covered
+    lpw, s = cw.f32_plan(1, 64, 3136, cu)
+    assert s > 1 and nl.workgroups(cw, "vectorized", 1, 64, 3136, cu) == (64 // lpw) * s
+    s = cw.plan_num_splits(1024, 3136, 1, cu)
+    lpw = cw.lib.xattn_f32_split_latents(1, 1024, 3136, s, cu)
+    assert s > 1 and nl.workgroups(cw, "splitk", 1, 1024, 3136, cu) == (1024 // lpw) * s
     assert math.ceil(1024 / cw.LATENTS_PER_WORKGROUP) == 16
 
 

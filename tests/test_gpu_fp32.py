@@ -71,12 +71,15 @@ def test_config3_batched_sweep(cw, oracle, b):
         fp32_gate(_events(cw, "vectorized", q, k, v), oracle.attention_f64(q, k, v))
 
 
-def test_growing_scores_force_rescales(cw, oracle):
+@pytest.mark.parametrize("b", [1, 100, 200])
+def test_growing_scores_force_rescales(cw, oracle, b):
     """Scores rise by ~12 per key across the key axis, so the running max grows
     far past the lazy-rescale threshold many times within one row.  At this
     shape launch_optimized_kernel splits the keys over workgroups, so the same
     inputs also run through launch_splitk_kernel with one split: one workgroup
-    walks all 200 keys and must rescale on the way."""
+    walks all 200 keys and must rescale on the way.  The batch (copies of one
+    element) sets the workgroup size: 16 latents at b=1, 32 at b=100, 64 at
+    b=200 on 256 compute units."""
     rng = np.random.RandomState(8)
     nl, ni = 40, 200
     u = rng.randn(768)
@@ -88,15 +91,19 @@ def test_growing_scores_force_rescales(cw, oracle):
          + 0.05 * rng.randn(ni, 768))[None].astype(np.float32)
     k = k[:, rng.permutation(ni)]  # rescales happen in every order
     v = rng.randn(1, ni, 768).astype(np.float32)
-    ref = oracle.attention_f64(q, k, v)
+    ref = np.repeat(oracle.attention_f64(q, k, v), b, axis=0)
+    order = np.argsort(k[0] @ u)
+    k_sorted, v_sorted = k[:, order], v[:, order]
+    q, k, v, k_sorted, v_sorted = (np.repeat(a, b, axis=0) for a in (q, k, v, k_sorted, v_sorted))
+    cu, _ = cw.device_info()
+    if cu == 256:
+        assert cw.lib.xattn_f32_split_latents(b, nl, ni, 1, cu) == {1: 16, 100: 32, 200: 64}[b]
     fp32_gate(_events(cw, "vectorized", q, k, v), ref)
-    k_sorted = k[:, np.argsort(k[0] @ u)]
-    v_sorted = v[:, np.argsort(k[0] @ u)]
     fp32_gate(_events(cw, "vectorized", q, k_sorted, v_sorted), ref)
     for kk, vv in ((k, v), (k_sorted, v_sorted)):
-        out, (po, pm, pl) = cw.splitk_partials(q, kk, vv, 1, nl, ni, 768, 1)
+        out, (po, pm, pl) = cw.splitk_partials(q, kk, vv, b, nl, ni, 768, 1)
         fp32_gate(out, ref)
-        fp32_gate(po.reshape(out.shape) / pl.reshape(1, nl, 1), ref)
+        fp32_gate(po.reshape(out.shape) / pl.reshape(b, nl, 1), ref)
 
 
 def test_special_cases(cw, oracle):
