@@ -254,12 +254,63 @@ int optimized_num_splits(int B, int NL, int NI, int cu) {
     return S;
 }
 
-// Launch shape of the 16-bit entry points: 64-latent workgroups (8
-// wavefronts) when they fill the device; else 32-latent ones (4
-// wavefronts), split over the keys only if those do not fill it either.
+// Modelled time (µs) of one 16-bit launch with nw wavefronts per workgroup
+// (8: 64 latents, 4: 32 latents) and S key splits of ct 32-key tiles each.
+// Fitted to launches on MI355X (256 CUs; 7 % mean error over B = 1..32,
+// N_latent = 64..1024, N_input = 784..50176): a 32-key tile costs a
+// workgroup 1.56 µs at 64 latents and 1.14 µs at 32, plus 5.45 µs per round
+// of workgroups (a round's Q loads and output stores reach HBM together); a
+// split launch adds the LSE merge, 1.86 µs + 0.31 µs per MB of partials
+// written and read back, + 0.06 µs per split while there are fewer merge rows
+// (B * N_latent) than CUs.
+static double h16_cost(int B, int NL, int cu, int nw, long long S, long long ct) {
+    const double tile_us = nw == 8 ? 1.559 : 1.140;
+    const long long W = (long long)B * h16_row_blocks(NL, nw) * S;
+    const long long rounds = (W + cu - 1) / cu;
+    double t = (double)rounds * ((double)ct * tile_us + 5.449);
+    if (S > 1) {
+        const double rows = (double)B * NL;
+        t += 1.862 + 0.308 * rows * (double)S * (kDim * 4) * 1e-6 +
+             0.061 * (double)S * std::max(0.0, 1.0 - rows / cu);
+    }
+    return t;
+}
+
+// Wavefronts per workgroup (8 or 4) for a 16-bit launch of S key splits of
+// `chunk` keys each: the cheaper by h16_cost.
+static int h16_shape_for(int B, int NL, int NI, int S, int chunk, int cu) {
+    const long long ct = NI > 0 ? ((long long)std::min(chunk, NI) + 31) / 32 : 0;
+    return h16_cost(B, NL, cu, 4, S, ct) < h16_cost(B, NL, cu, 8, S, ct) ? 4 : 8;
+}
+
+// Launch shape of the 16-bit entry points: the (wavefronts, S) pair of least
+// h16_cost, S up to min(tiles, cu) whole 32-key tiles per split.  The last
+// shape is cached per thread.
 static void wmma_plan(int B, int NL, int NI, int cu, int* nw, int* S) {
-    *nw = (long long)B * h16_row_blocks(NL, 8) >= cu ? 8 : 4;
-    *S = plan_splits(B, NL, NI, cu, 8 * *nw, 32);
+    thread_local int key[4] = {-1, -1, -1, -1}, val[2] = {8, 1};
+    if (key[0] == B && key[1] == NL && key[2] == NI && key[3] == cu) {
+        *nw = val[0];
+        *S = val[1];
+        return;
+    }
+    int bw = 8, bs = 1;
+    const long long tiles = NI > 0 ? ((long long)NI + 31) / 32 : 0;
+    if (B > 0 && NL > 0 && tiles > 0) {
+        double best_t = -1.0;
+        const long long smax = std::min<long long>(tiles, cu);
+        for (int w = 8; w >= 4; w -= 4) {
+            for (long long s = 1; s <= smax; ++s) {
+                const long long ct = (tiles + s - 1) / s;
+                if ((tiles + ct - 1) / ct != s) continue;  // same chunks as a smaller s
+                const double t = h16_cost(B, NL, cu, w, s, ct);
+                if (best_t < 0.0 || t < best_t) best_t = t, bw = w, bs = (int)s;
+            }
+        }
+    }
+    key[0] = B, key[1] = NL, key[2] = NI, key[3] = cu;
+    val[0] = bw, val[1] = bs;
+    *nw = bw;
+    *S = bs;
 }
 
 // Library-workspace split launch shared by the fp32 and 16-bit entry points.
@@ -345,6 +396,15 @@ int xattn_f32_split_latents(int batch_size, int N_latent, int N_input, int num_s
     const int chunk = (int)(((long long)std::max(N_input, 0) + num_splits - 1) / num_splits);
     return 64 / f32_parts(batch_size, N_latent, N_input, num_splits, chunk,
                           cu_count < 1 ? 1 : cu_count);
+}
+
+int xattn_wmma_split_latents(int batch_size, int N_latent, int N_input, int num_splits,
+                             int cu_count) {
+    if (batch_size < 1 || N_latent < 1 || num_splits < 1) return 64;
+    long long chunk = ((long long)std::max(N_input, 0) + num_splits - 1) / num_splits;
+    chunk = (chunk + 15) / 16 * 16;
+    return 8 * h16_shape_for(batch_size, N_latent, N_input, num_splits, (int)chunk,
+                             cu_count < 1 ? 1 : cu_count);
 }
 
 void xattn_wmma_plan(int batch_size, int N_latent, int N_input, int cu_count,
@@ -486,7 +546,9 @@ static void wmma_splitk_common(bool bf16, const char* who, const uint16_t* Q, co
     // kernel_wmma_splitk.cu:52: chunk = ceil(NI / S) rounded up to a multiple of 16
     long long chunk = ((long long)N_input + num_splits - 1) / num_splits;
     chunk = (chunk + 15) / 16 * 16;
-    if (!launch_flash16(bf16, 8, Q, K, V, nullptr, po, pm, pl, batch_size, N_latent, N_input,
+    const int nw = h16_shape_for(batch_size, N_latent, N_input, num_splits, (int)chunk,
+                                 device_cu_count());
+    if (!launch_flash16(bf16, nw, Q, K, V, nullptr, po, pm, pl, batch_size, N_latent, N_input,
                         num_splits, (int)chunk, stream))
         return;
     launch_lse_combine(po, pm, pl, output, batch_size * N_latent, num_splits, stream);

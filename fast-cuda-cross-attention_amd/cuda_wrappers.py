@@ -150,6 +150,8 @@ lib.xattn_f32_plan.argtypes = [_I, _I, _I, _I, ctypes.POINTER(_I), ctypes.POINTE
 lib.xattn_f32_plan.restype = None
 lib.xattn_f32_split_latents.argtypes = [_I, _I, _I, _I, _I]
 lib.xattn_f32_split_latents.restype = ctypes.c_int
+lib.xattn_wmma_split_latents.argtypes = [_I, _I, _I, _I, _I]
+lib.xattn_wmma_split_latents.restype = ctypes.c_int
 
 # Workgroup shape of the MFMA kernels (csrc/xattn_flash_*.hip): 64 latents per
 # workgroup (the fp32 entry points drop to 32 or 16, the 16-bit ones to 32,
@@ -173,8 +175,8 @@ def f32_plan(batch_size, N_latent, N_input, sm_count):
 
 def wmma_plan(batch_size, N_latent, N_input, sm_count):
     """(latents per workgroup, key splits) of launch_wmma_kernel and its bf16
-    twin: 64-latent workgroups when they fill ``sm_count`` compute units, else
-    32-latent ones, split over the keys only if those do not fill it."""
+    twin: 64- or 32-latent workgroups and whole-tile key splits, chosen by
+    the library's cost model."""
     lpw, s = _I(0), _I(0)
     lib.xattn_wmma_plan(batch_size, N_latent, N_input, int(sm_count), ctypes.byref(lpw),
                         ctypes.byref(s))
@@ -182,16 +184,17 @@ def wmma_plan(batch_size, N_latent, N_input, sm_count):
 
 
 def plan_num_splits(N_latent, N_input, batch_size, sm_count, keys_per_tile=KEYS_PER_TILE_F32):
-    """Default num_splits of the split-K drivers, each split a whole number of
-    tiles: for fp32 (16-key tiles) the splits of f32_plan, whose workgroup
-    size launch_splitk_kernel then picks again; for the 16-bit split-K kernels
-    (32-key tiles) enough splits for 64-latent workgroups to fill
-    ``sm_count`` compute units once.  (The
-    reference's ``choose_num_splits`` sizes for 4-latent blocks and 4x
-    oversubscription; it is kept unchanged for callers that use it
-    directly.)"""
+    """Default num_splits of the split-K drivers: the splits the library's
+    own plan takes for the shape -- f32_plan's for fp32 (16-key tiles),
+    wmma_plan's for the 16-bit kernels (32-key tiles) -- whose workgroup
+    size launch_splitk_kernel / launch_wmma_splitk_kernel then pick again for
+    that num_splits.  (The reference's ``choose_num_splits`` sizes for
+    4-latent blocks and 4x oversubscription; it is kept unchanged for callers
+    that use it directly.)"""
     if keys_per_tile == KEYS_PER_TILE_F32:
         return max(1, f32_plan(batch_size, N_latent, N_input, sm_count)[1])
+    if keys_per_tile == KEYS_PER_TILE_F16:
+        return max(1, wmma_plan(batch_size, N_latent, N_input, sm_count)[1])
     return max(1, lib.xattn_plan_splits(batch_size, N_latent, N_input, int(sm_count),
                                         LATENTS_PER_WORKGROUP, keys_per_tile))
 

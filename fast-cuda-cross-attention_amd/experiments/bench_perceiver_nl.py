@@ -46,8 +46,8 @@ def workgroups(cw, impl, B, nl, ni, cu):
         s = cw.plan_num_splits(nl, ni, B, cu)
         return math.ceil(nl / cw.lib.xattn_f32_split_latents(B, nl, ni, s, cu)) * B * s
     if impl.startswith("wmma_splitk"):
-        tile = cw.KEYS_PER_TILE_F16
-        return rows * cw.lib.xattn_plan_splits(B, nl, ni, cu, cw.LATENTS_PER_WORKGROUP, tile)
+        s = cw.plan_num_splits(nl, ni, B, cu, cw.KEYS_PER_TILE_F16)
+        return math.ceil(nl / cw.lib.xattn_wmma_split_latents(B, nl, ni, s, cu)) * B * s
     if impl.startswith("wmma"):
         lpw, s = cw.wmma_plan(B, nl, ni, cu)
         return math.ceil(nl / lpw) * B * s

@@ -166,12 +166,17 @@ void xattn_f32_plan(int batch_size, int N_latent, int N_input, int cu_count,
 int xattn_f32_split_latents(int batch_size, int N_latent, int N_input, int num_splits,
                             int cu_count);
 /* Launch shape launch_wmma_kernel / launch_wmma_bf16_kernel use (no
- * reference counterpart): 64-latent workgroups when batch_size *
- * ceil(N_latent / 64) fills cu_count compute units, else 32-latent ones,
- * split over the keys (32-key tiles) only if those do not fill it either.
+ * reference counterpart): latents per workgroup (64 on 8 wavefronts, or 32
+ * on 4) and key splits (32-key tiles, whole tiles per split), chosen by a
+ * cost model of the 16-bit kernel and the merge fitted to MI355X launches.
  * Writes the latents per workgroup and the number of key splits. */
 void xattn_wmma_plan(int batch_size, int N_latent, int N_input, int cu_count,
                      int* latents_per_workgroup, int* num_splits);
+/* Latents per workgroup launch_wmma_splitk_kernel and its bf16 twin use for
+ * num_splits key splits (64 or 32, by the cost model of xattn_wmma_plan; no
+ * reference counterpart). */
+int xattn_wmma_split_latents(int batch_size, int N_latent, int N_input, int num_splits,
+                             int cu_count);
 
 #ifdef __cplusplus
 }

@@ -123,3 +123,35 @@ def test_growing_scores_force_restarts(cw, oracle, bf16):
         one, _ = cw.wmma_splitk_partials(q, kp, vp, 1, nl, ni, 768, 1, bf16=bf16)
         tight = oracle.rel_err(one, ref)
         assert np.all(np.isfinite(one)) and tight <= 2 * TIGHT[bf16], tight
+
+
+@pytest.mark.parametrize("bf16", [False, True], ids=["fp16", "bf16"])
+def test_wide_workgroups_split_and_restart(cw, oracle, bf16):
+    """Split-K partials and pass restarts on 64-latent workgroups: 64 copies
+    of an 80-latent, 400-key problem whose scores rise by ~0.62 per key in
+    exp2 units, keys in rising order, in two splits (208 and 192 keys).
+    64 x 2 row blocks x 2 splits fill 256 CUs once with 64-latent workgroups
+    (32-latent ones would need two rounds), so the split-K entry takes the
+    8-wavefront kernel; each split spans over 118 exp2 units, past both
+    types' restart bound."""
+    rng = np.random.RandomState(9)
+    b, nl, ni = 64, 80, 400
+    u = rng.randn(768)
+    u /= np.linalg.norm(u)
+    q = (u * np.sqrt(768.0) * (1.0 + 0.01 * rng.randn(nl, 1))
+         + 0.1 * rng.randn(nl, 768))[None].astype(np.float32)
+    k = (np.arange(ni)[:, None] * (12.0 / np.sqrt(768.0)) * u
+         + 0.05 * rng.randn(ni, 768))[None].astype(np.float32)
+    v = rng.randn(1, ni, 768).astype(np.float32)
+    ref = np.repeat(_rounded_ref(oracle, cw, q, k, v, bf16), b, axis=0)
+    qb, kb, vb = (np.repeat(a, b, axis=0) for a in (q, k, v))
+    cu, _ = cw.device_info()
+    if cu == 256:
+        assert cw.lib.xattn_wmma_split_latents(b, nl, ni, 2, cu) == 64
+    out, (po, pm, pl) = cw.wmma_splitk_partials(qb, kb, vb, b, nl, ni, 768, 2, bf16=bf16)
+    tight = oracle.rel_err(out, ref)
+    assert np.all(np.isfinite(out)) and tight <= 2 * TIGHT[bf16], tight
+    # both splits are live and every batch copy holds the same partials
+    assert np.all(pm > -oracle.FLT_MAX) and np.all(pl > 0)
+    pm = pm.reshape(b, nl, 2)
+    assert np.array_equal(pm, np.broadcast_to(pm[:1], pm.shape))
