@@ -41,6 +41,7 @@
 // kernel_splitk.cu:94-180).
 
 #include "xattn_common.h"
+#include "xattn_launch.h"
 
 namespace xattn {
 namespace f32 {
@@ -364,18 +365,25 @@ void flash_f32_kernel(Params p) {
 }
 
 // Log-sum-exp merge of split partials (kernel_splitk.cu:186-236).  One
-// workgroup of 192 threads per (batch, latent) row: each wave first reduces
-// M = max pm and L = sum exp(pm - M) pl over the splits (lane-strided), then
-// thread c accumulates float4 column c over the splits with 8 partial rows in
-// flight at a time.  HBM-bound: reads S * 3 KiB of po per row.
-constexpr int kCombineThreads = kDim / 4;  // 192
+// workgroup per (batch, latent) row, in P groups of 192 threads: every wave
+// first reduces M = max pm and L = sum exp(pm - M) pl over the splits
+// (lane-strided), then thread c of group p accumulates float4 column c over
+// splits p, p + P, ... with 8 partial rows in flight at a time, and the P
+// group sums are added in group order through LDS.  P = 1 when there are
+// enough rows to fill the device (HBM-bound: S * 3 KiB of po per row); P = 4
+// for fewer rows, where one group's chain of dependent loads would set the
+// time.
+constexpr int kCombineThreads = kDim / 4;  // 192 threads per group
 
-__global__ __launch_bounds__(kCombineThreads)
+template <int P>
+__global__ __launch_bounds__(kCombineThreads * P)
 void lse_combine_kernel(const float* __restrict__ po, const float* __restrict__ pm,
                         const float* __restrict__ pl, float* __restrict__ out, int S) {
+    __shared__ f4 part[P > 1 ? (P - 1) * kCombineThreads : 1];
     const size_t row = blockIdx.x;
     const int lane = threadIdx.x & 63;
-    const int c = threadIdx.x;
+    const int c = threadIdx.x % kCombineThreads;
+    const int grp = threadIdx.x / kCombineThreads;
     const float* pmr = pm + row * S;
     const float* plr = pl + row * S;
 
@@ -389,25 +397,31 @@ void lse_combine_kernel(const float* __restrict__ po, const float* __restrict__ 
     }
     L = wave_sum(L);
 
+    // Batches of 8 splits per thread; a partial last batch re-reads split
+    // S - 1 with weight 0, so every batch issues its 8 loads before the first
+    // use (no chain of dependent single loads).
     const f4* src = (const f4*)(po + row * S * kDim) + c;
     f4 acc = {0.f, 0.f, 0.f, 0.f};
-    int s = 0;
-    for (; s + 8 <= S; s += 8) {
+    for (int s = grp; s < S; s += 8 * P) {
         f4 v[8];
         float wgt[8];
 #pragma unroll
         for (int u = 0; u < 8; ++u) {
-            v[u] = src[(size_t)(s + u) * (kDim / 4)];
-            const float m = pmr[s + u];
-            wgt[u] = (m == -FLT_MAX) ? 0.f : expf(m - M);
+            const int i = s + u * P;
+            const int ic = i < S ? i : S - 1;
+            v[u] = src[(size_t)ic * (kDim / 4)];
+            const float m = pmr[ic];
+            wgt[u] = (i >= S || m == -FLT_MAX) ? 0.f : expf(m - M);
         }
 #pragma unroll
         for (int u = 0; u < 8; ++u) acc += wgt[u] * v[u];
     }
-    for (; s < S; ++s) {
-        const float m = pmr[s];
-        if (m == -FLT_MAX) continue;
-        acc += expf(m - M) * src[(size_t)s * (kDim / 4)];
+    if constexpr (P > 1) {
+        if (grp > 0) part[(grp - 1) * kCombineThreads + c] = acc;
+        __syncthreads();
+        if (grp > 0) return;
+#pragma unroll
+        for (int q = 1; q < P; ++q) acc += part[(q - 1) * kCombineThreads + c];
     }
     ((f4*)(out + row * kDim))[c] = acc * (1.0f / (L + 1e-6f));
 }
@@ -455,8 +469,12 @@ bool launch_flash_f32(int ds, const float* Q, const float* K, const float* V, fl
 bool launch_lse_combine(const float* po, const float* pm, const float* pl, float* out,
                         int rows, int S, hipStream_t stream) {
     if (rows <= 0) return true;
-    hipLaunchKernelGGL(f32::lse_combine_kernel, dim3(rows), dim3(f32::kCombineThreads), 0,
-                       stream, po, pm, pl, out, S);
+    if (rows < device_cu_count() && S > 1)
+        hipLaunchKernelGGL(f32::lse_combine_kernel<4>, dim3(rows), dim3(4 * f32::kCombineThreads),
+                           0, stream, po, pm, pl, out, S);
+    else
+        hipLaunchKernelGGL(f32::lse_combine_kernel<1>, dim3(rows), dim3(f32::kCombineThreads), 0,
+                           stream, po, pm, pl, out, S);
     return check_launch("lse_combine");
 }
 
