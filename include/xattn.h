@@ -54,10 +54,10 @@ void launch_tiled_kernel(const float* Q, const float* K, const float* V,
 /* Replaces launch_optimized_kernel, kernel_vectorized.cu:198-208 (the
  * 'vectorized' entry of cuda_wrappers.py:352-357).  Both GEMMs on fp32 MFMA
  * (v_mfma_f32_16x16x4_f32), online softmax in registers.  dim == 768.
- * When batch_size * ceil(N_latent / 64) cannot fill the device it splits the
- * keys internally and merges with a log-sum-exp pass; the partials then live
- * in a library-owned device workspace that is allocated on first need and
- * grown (never shrunk) per device. */
+ * Workgroups of 64, 32 or 16 latents and, where those cannot fill the device
+ * cheaply, key splits merged by a log-sum-exp pass, as xattn_f32_plan
+ * reports; split partials live in a library-owned device workspace that is
+ * allocated on first need and grown (never shrunk) per device. */
 void launch_optimized_kernel(const float* Q, const float* K, const float* V,
                              float* output, int batch_size, int N_latent,
                              int N_input, int dim, hipStream_t stream);
@@ -80,7 +80,8 @@ void launch_splitk_kernel(const float* Q, const float* K, const float* V,
 
 /* Replaces launch_wmma_kernel, kernel_wmma.cu:139-154.  Q, K, V are IEEE
  * binary16 bit patterns; Q is pre-scaled by 1/sqrt(dim) by the caller
- * (cuda_wrappers.py:635-640).  dim == 768. */
+ * (cuda_wrappers.py:635-640).  dim == 768.  Launch shape and internal key
+ * splits (library workspace, as above) as xattn_wmma_plan reports. */
 void launch_wmma_kernel(const uint16_t* Q, const uint16_t* K,
                         const uint16_t* V, float* output, int batch_size,
                         int N_latent, int N_input, int dim,
