@@ -200,8 +200,13 @@ void flash_f32_kernel(Params p) {
     // score outgrows the pass's reference.
     auto softmax = [&](f4 s, int n0) {
         float x[4];
+        if (n0 + BN <= k1) {  // a full tile (uniform branch): no key to mask
 #pragma unroll
-        for (int i = 0; i < 4; ++i) x[i] = (n0 + 4 * g + i < k1) ? s[i] : -INFINITY;
+            for (int i = 0; i < 4; ++i) x[i] = s[i];
+        } else {
+#pragma unroll
+            for (int i = 0; i < 4; ++i) x[i] = (n0 + 4 * g + i < k1) ? s[i] : -INFINITY;
+        }
         float tmax = fmaxf(fmaxf(x[0], x[1]), fmaxf(x[2], x[3]));
         tmax = wave_max16_groups(tmax);
         m_true = fmaxf(m_true, tmax);
