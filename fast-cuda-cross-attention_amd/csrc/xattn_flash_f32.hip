@@ -37,7 +37,7 @@
 // keys again with m_ref = the max seen so far; unit-variance scores never
 // need a second pass.  The exact max is tracked separately and folded in at
 // the end, so the normalised output and the split partials (pm = exact max
-// score) match the reference algorithm (kernel_vectorized.cu:277-181,
+// score) match the reference algorithm (kernel_vectorized.cu:58-181,
 // kernel_splitk.cu:94-180).
 
 #include "xattn_common.h"

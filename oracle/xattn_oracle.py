@@ -171,12 +171,12 @@ def sdpa_cpu(q, k, v, threads=None):
 # ---------------------------------------------------------------------------
 
 def online_softmax_f64(q, k, v, tile=16, eps=1e-6):
-    """Tile-by-tile running max / running sum, as kernel_vectorized.cu:251-381.
+    """Tile-by-tile running max / running sum, as kernel_vectorized.cu:58-181.
 
     For each key tile: new_max = max(running_max, tile_max); the accumulator
     and running sum are rescaled by exp(running_max - new_max); tile weights
     exp(s - new_max) are summed and applied to V.  The result is normalised by
-    1 / (running_sum + eps) (kernel_vectorized.cu:367).  float64.
+    1 / (running_sum + eps) (kernel_vectorized.cu:181).  float64.
     """
     q = _as3(q).astype(np.float64)
     k = _as3(k).astype(np.float64)
