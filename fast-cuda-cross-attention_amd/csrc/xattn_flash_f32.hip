@@ -18,6 +18,14 @@
 // files inside the loop.  One wavefront per SIMD; the MFMA pipe is kept busy
 // by a single wave.
 //
+// Column-split forms (DS = 2 or 4) for batch sizes and latent counts whose
+// 64-latent workgroups would leave compute units idle: DS wavefronts share
+// one 16-latent block, each holding 768 / DS columns of Q^T and O (so a
+// workgroup covers 32 or 16 latents); after QK each writes its share of S^T
+// to LDS and, after the next barrier, every wavefront of the block adds the
+// DS shares in the same order before its softmax.  The launch planner picks
+// the form and the key splits (xattn_abi.hip, f32_plan).
+//
 // K and V tiles are shared by the 4 wavefronts through LDS and arrive by
 // global->LDS DMA (16 B per lane, 1 KiB per wave instruction).  Phases
 // alternate QK(t), PV(t); phase p reads buffer p % 3, and the data of phase
