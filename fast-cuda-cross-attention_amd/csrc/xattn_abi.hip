@@ -76,38 +76,89 @@ int device_cu_count() {
 }
 
 // --------------------------------------------------------------------------
-// Library-owned split workspace for launch_optimized_kernel (grow-only).
+// Library-owned split workspace of launch_optimized_kernel and
+// launch_wmma_kernel / launch_wmma_bf16_kernel: one grow-only buffer per
+// device, released with the process.  A split launch leases it from acquire
+// to release (the lock is held in between, so another host thread cannot
+// enqueue work on the buffer meanwhile); when the launch runs on another
+// stream than the previous split launch, that stream first waits for the
+// event recorded after the previous launch's merge, so work on different
+// streams never uses the buffer at the same time.
 // --------------------------------------------------------------------------
+struct Workspace {
+    void* ptr = nullptr;
+    size_t bytes = 0;
+    hipEvent_t done = nullptr;   // recorded after the last split launch's merge
+    hipStream_t last = nullptr;  // the stream of that launch
+    bool used = false;
+};
 static std::mutex g_ws_mu;
-static void* g_ws_ptr[256];
-static size_t g_ws_bytes[256];
+static Workspace g_ws[256];
 
-static void* workspace(size_t bytes) {
-    int dev = 0;
-    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 256) {
-        set_error(XATTN_ERR_ALLOC, "workspace: no current device");
-        return nullptr;
-    }
-    std::lock_guard<std::mutex> lk(g_ws_mu);
-    if (g_ws_bytes[dev] < bytes) {
-        if (g_ws_ptr[dev]) {
-            // Earlier launches may still read the old block.
-            (void)hipDeviceSynchronize();
-            (void)hipFree(g_ws_ptr[dev]);
-            g_ws_ptr[dev] = nullptr;
-            g_ws_bytes[dev] = 0;
-        }
-        void* p = nullptr;
-        if (hipMalloc(&p, bytes) != hipSuccess) {
-            (void)hipGetLastError();
-            set_error(XATTN_ERR_ALLOC, "workspace: hipMalloc(%zu) failed", bytes);
+class WorkspaceLease {
+  public:
+    // The device's workspace of at least `bytes`, ordered after its previous
+    // user; nullptr (error recorded) on failure.
+    void* acquire(size_t bytes, hipStream_t stream) {
+        int dev = 0;
+        if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 256) {
+            set_error(XATTN_ERR_ALLOC, "workspace: no current device");
             return nullptr;
         }
-        g_ws_ptr[dev] = p;
-        g_ws_bytes[dev] = bytes;
+        lk_.lock();
+        dev_ = dev;
+        Workspace& w = g_ws[dev];
+        if (w.bytes < bytes) {
+            if (w.ptr) {
+                // Earlier launches may still read the old block.
+                (void)hipDeviceSynchronize();
+                (void)hipFree(w.ptr);
+                w.ptr = nullptr;
+                w.bytes = 0;
+                w.used = false;
+            }
+            void* p = nullptr;
+            if (hipMalloc(&p, bytes) != hipSuccess) {
+                (void)hipGetLastError();
+                set_error(XATTN_ERR_ALLOC, "workspace: hipMalloc(%zu) failed", bytes);
+                return nullptr;
+            }
+            w.ptr = p;
+            w.bytes = bytes;
+        }
+        if (!w.done && hipEventCreateWithFlags(&w.done, hipEventDisableTiming) != hipSuccess) {
+            (void)hipGetLastError();
+            w.done = nullptr;
+            set_error(XATTN_ERR_ALLOC, "workspace: hipEventCreateWithFlags failed");
+            return nullptr;
+        }
+        if (w.used && w.last != stream && hipStreamWaitEvent(stream, w.done, 0) != hipSuccess) {
+            (void)hipGetLastError();
+            set_error(XATTN_ERR_LAUNCH, "workspace: hipStreamWaitEvent failed");
+            return nullptr;
+        }
+        return w.ptr;
     }
-    return g_ws_ptr[dev];
-}
+    // The buffer is now in use by the work enqueued on `stream`.
+    void release(hipStream_t stream) {
+        if (dev_ < 0 || !lk_.owns_lock()) return;
+        Workspace& w = g_ws[dev_];
+        if (hipEventRecord(w.done, stream) == hipSuccess) {
+            w.last = stream;
+            w.used = true;
+        } else {
+            (void)hipGetLastError();
+            // Without the event the next user must not overlap this one.
+            (void)hipStreamSynchronize(stream);
+            w.used = false;
+        }
+        lk_.unlock();
+    }
+
+  private:
+    std::unique_lock<std::mutex> lk_{g_ws_mu, std::defer_lock};
+    int dev_ = -1;
+};
 
 // --------------------------------------------------------------------------
 // Validation
@@ -320,11 +371,12 @@ struct SplitScratch {
     float* pl;
 };
 
-static bool split_scratch(SplitScratch* s, int B, int NL, int S) {
+static bool split_scratch(SplitScratch* s, WorkspaceLease& lease, int B, int NL, int S,
+                          hipStream_t stream) {
     const size_t rows = (size_t)B * NL;
     const size_t po_bytes = rows * S * kDim * sizeof(float);
     const size_t ml_bytes = rows * S * sizeof(float);
-    char* ws = (char*)workspace(po_bytes + 2 * ml_bytes + 256);
+    char* ws = (char*)lease.acquire(po_bytes + 2 * ml_bytes + 256, stream);
     if (!ws) return false;
     s->po = (float*)ws;
     s->pm = (float*)(ws + po_bytes);
@@ -476,11 +528,12 @@ void launch_optimized_kernel(const float* Q, const float* K, const float* V, flo
     const int tiles = (N_input + 15) / 16;
     const int chunk = ((tiles + S - 1) / S) * 16;
     SplitScratch sc;
-    if (!split_scratch(&sc, batch_size, N_latent, S)) return;
-    if (!launch_flash_f32(ds, Q, K, V, nullptr, sc.po, sc.pm, sc.pl, batch_size, N_latent,
-                          N_input, S, chunk, stream))
-        return;
-    launch_lse_combine(sc.po, sc.pm, sc.pl, output, batch_size * N_latent, S, stream);
+    WorkspaceLease lease;
+    if (!split_scratch(&sc, lease, batch_size, N_latent, S, stream)) return;
+    if (launch_flash_f32(ds, Q, K, V, nullptr, sc.po, sc.pm, sc.pl, batch_size, N_latent,
+                         N_input, S, chunk, stream))
+        launch_lse_combine(sc.po, sc.pm, sc.pl, output, batch_size * N_latent, S, stream);
+    lease.release(stream);
 }
 
 void launch_splitk_kernel(const float* Q, const float* K, const float* V, float* output,
@@ -523,11 +576,12 @@ static void wmma_common(bool bf16, const char* who, const uint16_t* Q, const uin
     const int tiles = (N_input + 31) / 32;
     const int chunk = ((tiles + S - 1) / S) * 32;
     SplitScratch sc;
-    if (!split_scratch(&sc, batch_size, N_latent, S)) return;
-    if (!launch_flash16(bf16, nw, Q, K, V, nullptr, sc.po, sc.pm, sc.pl, batch_size, N_latent,
-                        N_input, S, chunk, stream))
-        return;
-    launch_lse_combine(sc.po, sc.pm, sc.pl, output, batch_size * N_latent, S, stream);
+    WorkspaceLease lease;
+    if (!split_scratch(&sc, lease, batch_size, N_latent, S, stream)) return;
+    if (launch_flash16(bf16, nw, Q, K, V, nullptr, sc.po, sc.pm, sc.pl, batch_size, N_latent,
+                       N_input, S, chunk, stream))
+        launch_lse_combine(sc.po, sc.pm, sc.pl, output, batch_size * N_latent, S, stream);
+    lease.release(stream);
 }
 
 static void wmma_splitk_common(bool bf16, const char* who, const uint16_t* Q, const uint16_t* K,
