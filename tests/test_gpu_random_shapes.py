@@ -1,0 +1,53 @@
+"""Seeded random shapes through every launch plan: the fp32 and bf16 entry
+points choose their workgroup size (64 / 32 / 16 latents) and key splits
+from the shape, and the split-K entry points their workgroup size from the
+caller's num_splits, so random (B, N_latent, N_input, num_splits) draws reach
+plans the fixed-shape tests do not.  Each output is checked against the
+float64 oracle (fp32 gate, or 2e-2 relative on the rounded 16-bit inputs)."""
+
+import math
+
+import numpy as np
+import pytest
+
+from conftest import fp32_gate
+
+pytestmark = pytest.mark.gpu
+
+
+def _shapes(seed, n):
+    rng = np.random.RandomState(seed)
+    out = []
+    while len(out) < n:
+        b = int(rng.randint(1, 9))
+        nl = int(rng.randint(1, 400))
+        ni = int(rng.randint(1, 3000))
+        if b * nl * ni <= 400_000:  # keeps the float64 oracle to a fraction of a second
+            out.append((b, nl, ni, int(rng.randint(1, 65))))
+    return out
+
+
+SHAPES = _shapes(20261201, 16)
+
+
+@pytest.mark.parametrize("b,nl,ni,s", SHAPES)
+def test_fp32_plans(cw, oracle, b, nl, ni, s):
+    q, k, v = oracle.make_inputs(b, nl, ni, 768, seed=b * 7919 + nl * 31 + ni)
+    ref = oracle.attention_f64(q, k, v)
+    out, _, _ = cw.benchmark_kernel_events("vectorized", q, k, v, b, nl, ni, 768, warmup=0,
+                                           iters=1)
+    fp32_gate(out, ref)
+    out, _ = cw.splitk_partials(q, k, v, b, nl, ni, 768, min(s, ni))
+    fp32_gate(out, ref)
+
+
+@pytest.mark.parametrize("b,nl,ni,s", SHAPES)
+def test_bf16_plans(cw, oracle, b, nl, ni, s):
+    q, k, v = oracle.make_inputs(b, nl, ni, 768, seed=b * 7919 + nl * 31 + ni + 1)
+    qh, kh, vh = cw._half_inputs(q, k, v, b, 768, True)
+    f = oracle.bf16_bits_to_f32
+    ref = oracle.attention_f64(f(qh).astype(np.float64) * math.sqrt(768), f(kh), f(vh))
+    out, _, _ = cw.benchmark_wmma_bf16_events(q, k, v, b, nl, ni, 768, warmup=0, iters=1)
+    assert np.all(np.isfinite(out)) and oracle.rel_err(out, ref) < 2e-2
+    out, _ = cw.wmma_splitk_partials(q, k, v, b, nl, ni, 768, min(s, ni), bf16=True)
+    assert np.all(np.isfinite(out)) and oracle.rel_err(out, ref) < 2e-2
