@@ -51,9 +51,24 @@ def load_traffic():
         return None
 
 
+def _time_cpu(fn, seconds):
+    """(calls, elapsed s) of ``fn`` repeated for ~``seconds`` after 3 warmups."""
+    for _ in range(3):
+        fn()
+    n, t0 = 0, time.perf_counter()
+    while True:
+        fn()
+        n += 1
+        el = time.perf_counter() - t0
+        if (el >= seconds and n >= 5) or el >= 3 * seconds:
+            return n, el
+
+
 def cpu_baseline(seconds):
     """PyTorch CPU SDPA (the reference's CPU path) on a bounded sample: one
-    batch element of the headline workload, repeated for ~``seconds``."""
+    batch element of the headline workload, repeated for ~``seconds``.  The
+    reference's own bmm -> softmax -> bmm formulation (generate_references.py:
+    17-23) is timed beside it for a third of that, reported under "also"."""
     sys.path.insert(0, os.path.join(ROOT, "oracle"))
     import torch
     import xattn_oracle
@@ -61,24 +76,24 @@ def cpu_baseline(seconds):
     cores = len(os.sched_getaffinity(0))
     torch.set_num_threads(cores)
     q, k, v = xattn_oracle.make_inputs(1, NL, NI, D, seed=0)
-    for _ in range(3):
-        xattn_oracle.sdpa_cpu(q, k, v)
-    n, t0 = 0, time.perf_counter()
-    while True:
-        xattn_oracle.sdpa_cpu(q, k, v)
-        n += 1
-        el = time.perf_counter() - t0
-        if (el >= seconds and n >= 5) or el >= 3 * seconds:
-            break
-    per_call = el / n
+    flop = algorithmic_flop(1, NL, NI, D)
+    n, el = _time_cpu(lambda: xattn_oracle.sdpa_cpu(q, k, v), seconds)
+    n2, el2 = _time_cpu(lambda: xattn_oracle.attention_torch_f32(q, k, v), seconds / 3)
     return {
-        "value": algorithmic_flop(1, NL, NI, D) / per_call / 1e12,
+        "value": flop / (el / n) / 1e12,
         "unit": "TFLOP/s",
         "cores": torch.get_num_threads(),
         "kind": "port",
         "sample": (f"torch CPU scaled_dot_product_attention fp32 on B=1 of the workload "
                    f"(NL={NL} NI={NI} D={D}), {n} calls in {el:.1f} s, "
-                   f"{per_call * 1e3:.2f} ms/call"),
+                   f"{el / n * 1e3:.2f} ms/call"),
+        "also": {
+            "value": flop / (el2 / n2) / 1e12,
+            "unit": "TFLOP/s",
+            "sample": (f"torch CPU bmm -> /sqrt(D) -> softmax -> bmm fp32 (the reference's "
+                       f"oracle formulation), same input, {n2} calls in {el2:.1f} s, "
+                       f"{el2 / n2 * 1e3:.2f} ms/call"),
+        },
     }
 
 
