@@ -22,9 +22,10 @@
 //
 // Softmax by passes: a row's weights are exp2(s - m_ref) with m_ref fixed for
 // a pass (the row max of the first tile, shared by the two owners of the
-// block); a pass restarts when some score exceeds m_ref by tau_log2<T> (in
-// exp2 units), which bounds every weight by 2^tau_log2<T> in the MFMA's input
-// type.  The exact running max is kept apart and folded in at the end, so
+// block); when some score exceeds m_ref by tau_log2<T> (in exp2 units) the
+// pass is discarded at its end and the keys run again, so every weight of a
+// kept pass is bounded by 2^tau_log2<T> in the MFMA's input type.  The exact
+// running max is kept apart and folded in at the end, so
 // the normalised output and the split partials (pm = exact max) follow the
 // reference algorithm (kernel_wmma.cu:88-131, kernel_wmma_splitk.cu:80-139).
 //
@@ -287,12 +288,18 @@ void flash16_kernel(Params p) {
     if (tid == 0) restart_flag = 0;
 
     const float tau_raw = tau_log2<T> / kLog2e;
-    // Softmax state of the owned unit, for latent qo (replicated over g):
-    // m_true: exact running max over this key half; m_ref: the reference of
-    // the weights, the same for both halves of the latent and fixed for a
-    // pass; lsum: the half's sum of weights.
+    // Softmax state of the owned unit, for latent qo: m_true: exact running
+    // max over this lane's keys of the half; m_ref: the reference of the
+    // weights, the same for both halves of the latent and fixed for a pass;
+    // lsum: the sum of this lane's weights.  The four lanes of a latent are
+    // combined only where a whole-half value is needed (the first tile, a
+    // restart, the end), so the per-tile softmax has no cross-lane step.
     float m_true = -FLT_MAX, m_ref = -FLT_MAX, lsum;
     bool ref_set = false;  // the same at every lane of the workgroup
+    // Lanes with a score over the pass's bound (a lane mask, so scalar):
+    // the pass is checked once, at its end.  Its weights may then have
+    // overflowed, but the whole pass is discarded and run again.
+    unsigned long long over;
     f4 acc[CBW][DB];  // O^T[d0 + 16t + 4g + i][q0 + 16(2h + cl) + j]
 
     for (bool first = true;; first = false) {  // passes over the key range; a second is rare
@@ -303,7 +310,7 @@ void flash16_kernel(Params p) {
 #pragma unroll
             for (int t = 0; t < DB; ++t) acc[cl][t] = (f4){0.f, 0.f, 0.f, 0.f};
         lsum = 0.f;
-        bool restart = false;
+        over = 0;
 
         for (int tile = 0; tile < ntiles; ++tile) {
             const int n0 = tile * BN, lo = row_lo(tile);
@@ -344,27 +351,26 @@ void flash16_kernel(Params p) {
                 const int r = 16 * kbo + 4 * g + i;  // tile row; its key is n0 - lo + r
                 x[i] = (r >= lo && n0 - lo + r < nk) ? sv[i] : -INFINITY;
             }
-            float tmax = fmaxf(fmaxf(x[0], x[1]), fmaxf(x[2], x[3]));
-            tmax = wave_max16_groups(tmax);
+            const float tmax = fmaxf(fmaxf(x[0], x[1]), fmaxf(x[2], x[3]));
             m_true = fmaxf(m_true, tmax);
             if (!ref_set) {
                 // First tile of the kernel: the two owners of a latent block
                 // agree on the reference, the row max of the tile.
-                if (g == 0) stats[w * QB + j].x = tmax;
+                const float hmax = wave_max16_groups(tmax);
+                if (g == 0) stats[w * QB + j].x = hmax;
                 lds_barrier();
-                m_ref = fmaxf(tmax, stats[(w ^ 1) * QB + j].x);
+                m_ref = fmaxf(hmax, stats[(w ^ 1) * QB + j].x);
                 lds_barrier();
                 ref_set = true;
             }
-            if (__any(tmax > m_ref + tau_raw) && lane == 0) restart_flag = 1;
+            // any lane over the bound <=> the latent's row max over the bound
+            over |= __ballot(tmax > m_ref + tau_raw);
             float pw[4];
-            float rs = 0.f;
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
                 pw[i] = fast_exp2((x[i] - m_ref) * kLog2e);
-                rs += pw[i];
+                lsum += pw[i];
             }
-            lsum += wave_sum16_groups(rs);
             // this half of block cbo's P^T operand: bytes 8 kbo .. 8 kbo + 7 of each lane
             *(u2v*)((char*)pbuf + (size_t)(cbo * kWave + lane) * 16 + 8 * kbo) =
                 (u2v){pack2<T>(pw[0], pw[1]), pack2<T>(pw[2], pw[3])};
@@ -375,12 +381,6 @@ void flash16_kernel(Params p) {
             ph += 1;
             wait_vmcnt<CPW>();
             lds_barrier();
-            // Every wavefront sets the flag (if at all) before this barrier, so
-            // all read the same value.
-            if (__builtin_amdgcn_readfirstlane(restart_flag)) {
-                restart = true;
-                break;
-            }
             v8 pt[CBW];
 #pragma unroll
             for (int cl = 0; cl < CBW; ++cl)
@@ -411,16 +411,22 @@ void flash16_kernel(Params p) {
                 }
             }
         }
-        if (!restart) break;
-        // Some latent's scores outgrew its reference: drain the DMA (V(t + 1)
-        // may be in flight), clear the flag, and run the keys again with the
-        // reference raised to the max seen so far over both halves.
+        // Every wavefront raises the flag (if at all) before this barrier, so
+        // all of them read the same value.
+        if (over != 0 && lane == 0) restart_flag = 1;
+        lds_barrier();
+        if (!__builtin_amdgcn_readfirstlane(restart_flag)) break;
+        // Some latent's scores outgrew its reference: drain the DMA (the
+        // re-reads past the last phase may be in flight), clear the flag, and
+        // run the keys again with the reference raised to the max seen so far
+        // over both halves.
         wait_vmcnt<0>();
         lds_barrier();
         if (tid == 0) restart_flag = 0;
-        if (g == 0) stats[w * QB + j].x = m_true;
+        const float hmax = wave_max16_groups(m_true);
+        if (g == 0) stats[w * QB + j].x = hmax;
         lds_barrier();
-        m_ref = fmaxf(m_true, stats[(w ^ 1) * QB + j].x);
+        m_ref = fmaxf(hmax, stats[(w ^ 1) * QB + j].x);
         lds_barrier();
     }
     wait_vmcnt<0>();  // the re-reads issued past the last phase
@@ -430,6 +436,8 @@ void flash16_kernel(Params p) {
     // exact max).  A wavefront's m_ref is that of the block of its score
     // unit; the output blocks it accumulates are weighted by their own
     // blocks' m_ref.
+    m_true = wave_max16_groups(m_true);
+    lsum = wave_sum16_groups(lsum);
     if (g == 0) stats[w * QB + j] = make_float2(m_true, lsum);
     if (g == 0 && kbo == 0) sref[cbo * QB + j] = m_ref;
     lds_barrier();

@@ -39,11 +39,11 @@
 //
 // Softmax in raw dot-product units by passes: a row's weights are
 // exp2((s - m_ref) c2) with m_ref fixed for the whole pass (the row max of
-// the first tile), so the accumulator is never rescaled.  If a later score
-// exceeds m_ref by 2^64 in exp2 space the workgroup abandons the pass (a
-// flag in LDS, read by every wavefront after the same barrier) and runs the
-// keys again with m_ref = the max seen so far; unit-variance scores never
-// need a second pass.  The exact max is tracked separately and folded in at
+// the first tile), so the accumulator is never rescaled.  If a score
+// exceeds m_ref by 2^64 in exp2 space the workgroup discards the pass at its
+// end (a flag in LDS, read by every wavefront after the same barrier) and
+// runs the keys again with m_ref = the max seen so far; unit-variance scores
+// never need a second pass.  The exact max is tracked separately and folded in at
 // the end, so the normalised output and the split partials (pm = exact max
 // score) match the reference algorithm (kernel_vectorized.cu:58-181,
 // kernel_splitk.cu:94-180).
@@ -199,13 +199,22 @@ void flash_f32_kernel(Params p) {
     if (tid == 0) *restart_flag = 0;
     const float c2 = kLog2e / sqrtf((float)kDim);
     const float tau_raw = kTauLog2 / c2;
+    // m_true and lsum cover this lane's keys only (4g + i of every tile):
+    // the four lanes of a latent are combined once, at the end of the pass,
+    // so the per-tile softmax has no cross-lane step except on the tile
+    // that sets the pass's reference.
     float m_true = -FLT_MAX, m_ref = -FLT_MAX, lsum;
+    bool ref_set = false;  // the same at every lane of the workgroup
+    // Lanes with a score over the pass's bound (a lane mask, so scalar):
+    // the pass is checked once, at its end.  Its weights may then have
+    // overflowed, but the whole pass is discarded and run again.
+    unsigned long long over;
     f4 acc[NT][4];
     float pw[4];
 
     // Online softmax of one tile's scores s (lane (j, g): latent j, keys
-    // n0 + 4g + i) into the P operand pw; raises the restart flag when a
-    // score outgrows the pass's reference.
+    // n0 + 4g + i) into the P operand pw; notes the lanes whose scores
+    // outgrow the pass's reference.
     auto softmax = [&](f4 s, int n0) {
         float x[4];
         if (n0 + BN <= k1) {  // a full tile (uniform branch): no key to mask
@@ -215,18 +224,20 @@ void flash_f32_kernel(Params p) {
 #pragma unroll
             for (int i = 0; i < 4; ++i) x[i] = (n0 + 4 * g + i < k1) ? s[i] : -INFINITY;
         }
-        float tmax = fmaxf(fmaxf(x[0], x[1]), fmaxf(x[2], x[3]));
-        tmax = wave_max16_groups(tmax);
+        const float tmax = fmaxf(fmaxf(x[0], x[1]), fmaxf(x[2], x[3]));
+        if (!ref_set) {
+            // first tile of the kernel: the reference is the latent's row max
+            m_ref = wave_max16_groups(tmax);
+            ref_set = true;
+        }
         m_true = fmaxf(m_true, tmax);
-        if (m_ref == -FLT_MAX) m_ref = tmax;
-        if (__any(tmax > m_ref + tau_raw) && lane == 0) *restart_flag = 1;
-        float rs = 0.f;
+        // any lane over the bound <=> the latent's row max over the bound
+        over |= __ballot(tmax > m_ref + tau_raw);
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
             pw[i] = fast_exp2((x[i] - m_ref) * c2);
-            rs += pw[i];
+            lsum += pw[i];
         }
-        lsum += wave_sum16_groups(rs);
     };
 
     for (bool first = true;; first = false) {  // passes over the keys; a second is rare
@@ -239,7 +250,7 @@ void flash_f32_kernel(Params p) {
 #pragma unroll
             for (int c = 0; c < 4; ++c) acc[T][c] = (f4){0.f, 0.f, 0.f, 0.f};
         lsum = 0.f;
-        bool restart = false;
+        over = 0;
         for (int tile = 0; tile < ntiles; ++tile) {
             const int n0 = k0 + tile * BN;
             int ph = 2 * tile;
@@ -247,14 +258,6 @@ void flash_f32_kernel(Params p) {
             // ---------------- QK phase ----------------
             wait_vmcnt<CPW>();      // this phase landed; phase ph+1 may be in flight
             lds_barrier();
-            if constexpr (DS > 1) {
-                // The flag of the previous tile's softmax (set before this
-                // barrier by every wavefront that raises it).
-                if (tile > 0 && __builtin_amdgcn_readfirstlane(*restart_flag)) {
-                    restart = true;
-                    break;
-                }
-            }
             f4 s;
             {
                 // K operand reads run two 4-MFMA groups ahead; the sched_barrier
@@ -290,14 +293,7 @@ void flash_f32_kernel(Params p) {
             ph += 1;
             wait_vmcnt<CPW>();
             lds_barrier();
-            if constexpr (DS == 1) {
-                // Every wavefront sets the flag (if at all) before this barrier,
-                // so all of them leave the pass at the same tile.
-                if (__builtin_amdgcn_readfirstlane(*restart_flag)) {
-                    restart = true;
-                    break;
-                }
-            } else {
+            if constexpr (DS > 1) {
                 // Every wavefront of the block sums the shares in the same
                 // order, so all of them hold bit-identical scores and weights.
                 const float* xs = xch + ((w - dp) * kWave + lane) * 4;
@@ -328,26 +324,26 @@ void flash_f32_kernel(Params p) {
                 }
             }
         }
-        if constexpr (DS > 1) {
-            // the last tile's flag
-            if (!restart) {
-                lds_barrier();
-                restart = __builtin_amdgcn_readfirstlane(*restart_flag) != 0;
-            }
-        }
-        if (!restart) break;
-        // Some latent's scores outgrew its reference: drain the DMA (phase
-        // ph + 1 may be in flight), clear the flag, and run the keys again
-        // with the reference raised to the max seen so far.
+        // Every wavefront raises the flag (if at all) before this barrier, so
+        // all of them read the same value.
+        if (over != 0 && lane == 0) *restart_flag = 1;
+        lds_barrier();
+        if (!__builtin_amdgcn_readfirstlane(*restart_flag)) break;
+        // Some latent's scores outgrew its reference: drain the DMA (the
+        // re-reads past the last phase may be in flight), clear the flag, and
+        // run the keys again with the reference raised to the max seen so far.
         wait_vmcnt<0>();
         lds_barrier();
         if (tid == 0) *restart_flag = 0;
-        m_ref = m_true;
+        m_ref = wave_max16_groups(m_true);
         lds_barrier();
     }
 
     wait_vmcnt<0>();  // the re-reads issued past the last phase
 
+    // The latent's exact max and sum of weights over its four lanes.
+    m_true = wave_max16_groups(m_true);
+    lsum = wave_sum16_groups(lsum);
     // Fold the exact max back in: factor = exp(m_ref - m_true) <= 1.
     const float factor = fast_exp2((m_ref - m_true) * c2);
     float rowscale;
