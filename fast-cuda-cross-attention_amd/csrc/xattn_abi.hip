@@ -80,17 +80,21 @@ int device_cu_count() {
 // launch_wmma_kernel / launch_wmma_bf16_kernel: one grow-only buffer per
 // device, released with the process.  A split launch leases it from acquire
 // to release (the lock is held in between, so another host thread cannot
-// enqueue work on the buffer meanwhile); when the launch runs on another
-// stream than the previous split launch, that stream first waits for the
-// event recorded after the previous launch's merge, so work on different
-// streams never uses the buffer at the same time.
+// enqueue work on the buffer meanwhile).  Work on different streams never
+// uses the buffer at the same time: while every split launch has used one
+// stream, stream order alone serialises them and nothing is recorded (an
+// event after every launch measured 4.5 us per call at 64 latents x 784
+// keys); the first launch on another stream synchronises the device once,
+// and from then on an event is recorded after each launch's merge and the
+// next launch on a different stream waits for it.
 // --------------------------------------------------------------------------
 struct Workspace {
     void* ptr = nullptr;
     size_t bytes = 0;
-    hipEvent_t done = nullptr;   // recorded after the last split launch's merge
+    hipEvent_t done = nullptr;   // recorded after the last split launch's merge (multi)
     hipStream_t last = nullptr;  // the stream of that launch
     bool used = false;
+    bool multi = false;          // a second stream has used the buffer
 };
 static std::mutex g_ws_mu;
 static Workspace g_ws[256];
@@ -126,16 +130,28 @@ class WorkspaceLease {
             w.ptr = p;
             w.bytes = bytes;
         }
-        if (!w.done && hipEventCreateWithFlags(&w.done, hipEventDisableTiming) != hipSuccess) {
-            (void)hipGetLastError();
-            w.done = nullptr;
-            set_error(XATTN_ERR_ALLOC, "workspace: hipEventCreateWithFlags failed");
-            return nullptr;
-        }
-        if (w.used && w.last != stream && hipStreamWaitEvent(stream, w.done, 0) != hipSuccess) {
-            (void)hipGetLastError();
-            set_error(XATTN_ERR_LAUNCH, "workspace: hipStreamWaitEvent failed");
-            return nullptr;
+        if (w.used && w.last != stream) {
+            if (!w.multi) {
+                // The first change of stream: no event covers the earlier
+                // launches, so wait for all of them.
+                if (!w.done &&
+                    hipEventCreateWithFlags(&w.done, hipEventDisableTiming) != hipSuccess) {
+                    (void)hipGetLastError();
+                    w.done = nullptr;
+                    set_error(XATTN_ERR_ALLOC, "workspace: hipEventCreateWithFlags failed");
+                    return nullptr;
+                }
+                if (hipDeviceSynchronize() != hipSuccess) {
+                    (void)hipGetLastError();
+                    set_error(XATTN_ERR_LAUNCH, "workspace: hipDeviceSynchronize failed");
+                    return nullptr;
+                }
+                w.multi = true;
+            } else if (hipStreamWaitEvent(stream, w.done, 0) != hipSuccess) {
+                (void)hipGetLastError();
+                set_error(XATTN_ERR_LAUNCH, "workspace: hipStreamWaitEvent failed");
+                return nullptr;
+            }
         }
         return w.ptr;
     }
@@ -143,10 +159,9 @@ class WorkspaceLease {
     void release(hipStream_t stream) {
         if (dev_ < 0 || !lk_.owns_lock()) return;
         Workspace& w = g_ws[dev_];
-        if (hipEventRecord(w.done, stream) == hipSuccess) {
-            w.last = stream;
-            w.used = true;
-        } else {
+        w.last = stream;
+        w.used = true;
+        if (w.multi && hipEventRecord(w.done, stream) != hipSuccess) {
             (void)hipGetLastError();
             // Without the event the next user must not overlap this one.
             (void)hipStreamSynchronize(stream);
