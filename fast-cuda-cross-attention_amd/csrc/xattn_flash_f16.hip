@@ -459,13 +459,31 @@ void flash16_kernel(Params p) {
             }
         }
     }
+    // The output leaves through the tile ring, free since the barrier above
+    // (the DMA was drained after the loop): per latent block, each
+    // wavefront writes its 16 x 192 slice row-major into its own area, then
+    // reads it back row-contiguous, so every store instruction covers whole
+    // 128-byte lines of a row (the accumulator layout gives 64-byte halves).
+    constexpr int SROW = DW * 4 + 16;  // padded staging row (bytes)
+    static_assert(NW * QB * SROW <= NBUF * BUFB, "staging area");
+    char* const stage = lds + w * (QB * SROW);
 #pragma unroll
     for (int cl = 0; cl < CBW; ++cl) {
-        const int q = q0 + QB * (CBW * h + cl) + j;
-        if (q >= p.NL) continue;
-        float* dst = out_row(q) + d0 + 4 * g;
 #pragma unroll
-        for (int t = 0; t < DB; ++t) *(f4*)(dst + 16 * t) = acc[cl][t] * rsc[cl];
+        for (int t = 0; t < DB; ++t)
+            *(f4*)(stage + j * SROW + (16 * t + 4 * g) * 4) = acc[cl][t] * rsc[cl];
+        const int qb = q0 + QB * (CBW * h + cl);
+#pragma unroll
+        for (int k = 0; k < QB * DW / 4 / kWave; ++k) {
+            const int pc = k * kWave + lane;  // 16-byte piece of the slice
+            const int r = pc / (DW / 4), c = pc % (DW / 4);
+            const f4 o = *(const f4*)(stage + r * SROW + 16 * c);
+            if (qb + r >= p.NL) continue;
+            f4* const at = (f4*)(out_row(qb + r) + d0 + 4 * c);
+            // partials are read back by the merge; the output is not
+            if (PARTIAL) *at = o;
+            else __builtin_nontemporal_store(o, at);
+        }
     }
 }
 
