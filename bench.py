@@ -143,6 +143,22 @@ def time_launches(cw, launch, steps, warmup):
     return wall, per
 
 
+def launch_stats(per_ms):
+    """Per-launch event times (µs): mean, median, extremes and the means of
+    the first and last quarter of the timed launches (a clock that is still
+    ramping shows as a first quarter slower than the last)."""
+    us = np.asarray(per_ms, dtype=np.float64) * 1e3
+    q = max(1, len(us) // 4)
+    return {
+        "mean": round(float(us.mean()), 2),
+        "median": round(float(np.median(us)), 2),
+        "min": round(float(us.min()), 2),
+        "max": round(float(us.max()), 2),
+        "first_quarter_mean": round(float(us[:q].mean()), 2),
+        "last_quarter_mean": round(float(us[-q:].mean()), 2),
+    }
+
+
 def run_case(cw, name, steps, warmup):
     b, nl, ni, et, entry, q_std = CASES[name]
     cu, _ = cw.device_info()
@@ -154,27 +170,25 @@ def run_case(cw, name, steps, warmup):
         host = (q, k, v)
     else:
         host = cw._half_inputs(q, k, v, b, D, bf16=(et == "bf16"))
-    bufs = [cw._allocate_gpu_memory(a.nbytes) for a in host]
-    for a, p in zip(host, bufs):
-        cw._copy_to_gpu(a, p, a.nbytes)
-    out = cw._allocate_gpu_memory(b * nl * D * 4)
+    bufs = [cw.DeviceBuffer.holding(a) for a in host]
+    out = cw.DeviceBuffer(b * nl * D * 4).zero()
     extra = []
     stream = ctypes.c_void_p(0)
     fn = getattr(cw.lib, entry)
     note = {}
     if entry == "launch_splitk_kernel":
         s = cw.plan_num_splits(nl, ni, b, cu)
-        extra = [cw._allocate_gpu_memory(b * nl * s * D * 4),
-                 cw._allocate_gpu_memory(b * nl * s * 4), cw._allocate_gpu_memory(b * nl * s * 4)]
+        extra = [cw.DeviceBuffer(b * nl * s * D * 4), cw.DeviceBuffer(b * nl * s * 4),
+                 cw.DeviceBuffer(b * nl * s * 4)]
         note["num_splits"] = s
-        args = [cw._fptr(p) for p in bufs + [out] + extra] + [b, nl, ni, D, s, stream]
+        args = [p.f32 for p in bufs + [out] + extra] + [b, nl, ni, D, s, stream]
     elif et == "fp32":
-        args = [cw._fptr(p) for p in bufs + [out]] + [b, nl, ni, D, stream]
+        args = [p.f32 for p in bufs + [out]] + [b, nl, ni, D, stream]
     else:
-        args = bufs + [cw._fptr(out), b, nl, ni, D, stream]
+        args = [p.ptr for p in bufs] + [out.f32, b, nl, ni, D, stream]
     wall, per = time_launches(cw, lambda: fn(*args), steps, warmup)
     for p in bufs + [out] + extra:
-        cw._free_gpu_memory(p)
+        p.close()
     bpe = 4 if et == "fp32" else 2
     kern_ms = float(np.mean(per))
     flop = algorithmic_flop(b, nl, ni, D)
@@ -187,7 +201,8 @@ def run_case(cw, name, steps, warmup):
         "pct_of_mfma_peak": round(100 * flop / (kern_ms * 1e-3) / 1e12 / peak, 2),
         "gbs_algorithmic": round(byt / (kern_ms * 1e-3) / 1e9, 1),
         "pct_of_hbm_peak": round(100 * byt / (kern_ms * 1e-3) / 8.0e12, 2),
-        "ms_per_step_wall": round(wall * 1e3 / steps, 5), **note,
+        "ms_per_step_wall": round(wall * 1e3 / steps, 5),
+        "launch_us": launch_stats(per), **note,
     }
 
 
@@ -195,16 +210,13 @@ def copy_calibration(cw, mib, reps=5):
     """Plain device-to-device copy of `mib` MiB, `reps` times: reads and writes
     exactly mib MiB per copy, the reference point for FETCH_SIZE/WRITE_SIZE."""
     n = mib * 1024 * 1024
-    a = cw._allocate_gpu_memory(n)
-    b = cw._allocate_gpu_memory(n)
-    cw.cudart.cudaMemset(a, 1, n)
-    cw.cudart.cudaDeviceSynchronize()
-    for _ in range(reps):
-        if cw.cudart.hipMemcpy(b, a, n, 3) != 0:  # hipMemcpyDeviceToDevice
-            raise RuntimeError("hipMemcpy D2D failed")
-    cw.cudart.cudaDeviceSynchronize()
-    cw._free_gpu_memory(a)
-    cw._free_gpu_memory(b)
+    with cw.DeviceBuffer(n) as a, cw.DeviceBuffer(n) as b:
+        cw.cudart.hipMemset(a.ptr, 1, n)
+        cw.cudart.hipDeviceSynchronize()
+        for _ in range(reps):
+            if cw.cudart.hipMemcpy(b.ptr, a.ptr, n, 3) != 0:  # hipMemcpyDeviceToDevice
+                raise RuntimeError("hipMemcpy D2D failed")
+        cw.cudart.hipDeviceSynchronize()
     print(json.dumps({"copy_calibration_bytes_per_copy": n, "copies": reps}), flush=True)
 
 
@@ -218,6 +230,8 @@ def main():
     ap.add_argument("--case", choices=sorted(CASES), action="append",
                     help="run a secondary workload instead of the headline")
     ap.add_argument("--copy-calibration", type=int, metavar="MIB")
+    ap.add_argument("--launch-log", metavar="PATH",
+                    help="also write every timed launch's event time (µs) to PATH as JSON")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU: this build has no multi-GPU path "
@@ -239,14 +253,10 @@ def main():
     q = rng.randn(B, NL, D).astype(np.float32)
     k = rng.randn(B, NI, D).astype(np.float32)
     v = rng.randn(B, NI, D).astype(np.float32)
-    bufs = [cw._allocate_gpu_memory(a.nbytes) for a in (q, k, v)]
-    out_bytes = B * NL * D * 4
-    out = cw._allocate_gpu_memory(out_bytes)
-    for a, p in zip((q, k, v), bufs):
-        cw._copy_to_gpu(a, p, a.nbytes)
-    cw.cudart.cudaMemset(out, 0, out_bytes)
-    qp, kp, vp = (cw._fptr(p) for p in bufs)
-    op = cw._fptr(out)
+    bufs = [cw.DeviceBuffer.holding(a) for a in (q, k, v)]
+    out = cw.DeviceBuffer(B * NL * D * 4).zero()
+    qp, kp, vp = (p.f32 for p in bufs)
+    op = out.f32
     stream = ctypes.c_void_p(0)
 
     def launch():
@@ -255,6 +265,10 @@ def main():
     # Timed region: K back-to-back launches bracketed by a device sync; each
     # launch also bracketed by HIP events on the launch stream.
     wall, per = time_launches(cw, launch, args.steps, args.warmup)
+    if args.launch_log:
+        with open(args.launch_log, "w") as f:
+            json.dump({"steps": args.steps, "warmup": args.warmup,
+                       "launch_us": [round(x * 1e3, 3) for x in per]}, f)
 
     flop = algorithmic_flop(B, NL, NI, D)
     ms_per_step = wall * 1e3 / args.steps
@@ -264,10 +278,9 @@ def main():
 
     # spot-check the result of the timed launches against the float64 oracle
     # on a few rows (cheap; the full parity suite lives in tests/)
-    res = np.zeros((B, NL, D), np.float32)
-    cw._copy_from_gpu(out, res, out_bytes)
+    res = out.download((B, NL, D))
     for p in bufs + [out]:
-        cw._free_gpu_memory(p)
+        p.close()
     sys.path.insert(0, os.path.join(ROOT, "oracle"))
     import xattn_oracle
     rows = [0, 17, 31]
@@ -284,6 +297,7 @@ def main():
         "ms_per_step": round(ms_per_step, 5),
         "us_per_call": round(kern_ms * 1e3, 2),
         "pct_of_mfma_peak": round(100.0 * achieved / PEAK_FP32_MFMA_TFLOPS, 2),
+        "launch_us": launch_stats(per),
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,

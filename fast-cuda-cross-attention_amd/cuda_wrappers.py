@@ -20,6 +20,7 @@ can observe are additive:
   to be multiples of 16).
 """
 
+import contextlib
 import ctypes
 import math
 import os
@@ -50,8 +51,8 @@ def _load_hip():
             return ctypes.CDLL(path)
         except OSError as e:  # try the next candidate
             errs.append(f"{path}: {e}")
-    raise RuntimeError("Could not find the HIP runtime library (libamdhip64.so). "
-                       "Please ensure ROCm is installed. Tried: " + "; ".join(errs))
+    raise RuntimeError("libamdhip64.so (the HIP runtime of a ROCm install) did not load; "
+                       "tried " + "; ".join(errs))
 
 
 class _HipRuntime:
@@ -103,7 +104,7 @@ try:
     cudaMemcpyHostToDevice = 1   # hipMemcpyHostToDevice
     cudaMemcpyDeviceToHost = 2   # hipMemcpyDeviceToHost
 except Exception as e:
-    raise RuntimeError(f"Failed to load HIP runtime: {e}")
+    raise RuntimeError(f"HIP runtime unavailable: {e}")
 
 # ---------------------------------------------------------------------------
 # kernels.so
@@ -116,9 +117,9 @@ if not os.path.exists(KERNELS_SO) and os.path.exists("./kernels.so"):
 
 try:
     lib = ctypes.CDLL(KERNELS_SO)
-except OSError:
-    raise RuntimeError(f"Failed to load kernels.so ({KERNELS_SO}). Please compile the HIP "
-                       f"kernels first using 'make' in {_HERE}.")
+except OSError as e:
+    raise RuntimeError(f"kernels.so did not load from {KERNELS_SO} ({e}); build it with "
+                       f"'make -C {_HERE}'")
 
 _F = ctypes.POINTER(ctypes.c_float)
 _I = ctypes.c_int
@@ -213,25 +214,22 @@ _WMMA_ARGS = [_P, _P, _P, _F, _I, _I, _I, _I, _P]
 _SPLITK_ARGS = [_F, _F, _F, _F, _F, _F, _F, _I, _I, _I, _I, _I, _P]
 _WMMA_SPLITK_ARGS = [_P, _P, _P, _F, _F, _F, _F, _I, _I, _I, _I, _I, _P]
 
-# fp16 MFMA kernel: half* Q/K/V (passed as void*), float* output.
+# Optional entry points: a kernels.so built without them loads, and the flag
+# says which are there (the reference's convention, cuda_wrappers.py:136-175).
 HAS_WMMA = _bind_optional("launch_wmma_kernel", _WMMA_ARGS)
-# Split-K (key-parallel) kernel: Q/K/V/out + po/pm/pl scratch + num_splits.
 HAS_SPLITK = _bind_optional("launch_splitk_kernel", _SPLITK_ARGS)
-# fp16 MFMA split-K: half Q/K/V (void*) + float out/po/pm/pl + num_splits.
 HAS_WMMA_SPLITK = _bind_optional("launch_wmma_splitk_kernel", _WMMA_SPLITK_ARGS)
-# bf16 twins (additive)
 HAS_WMMA_BF16 = _bind_optional("launch_wmma_bf16_kernel", _WMMA_ARGS)
 HAS_WMMA_SPLITK_BF16 = _bind_optional("launch_wmma_splitk_bf16_kernel", _WMMA_SPLITK_ARGS)
 
 
 class DesignLimited(RuntimeError):
-    """Raised when a kernel cannot run a config by design (not a bug).
+    """A shape this build's kernel does not take, as a matter of design.
 
-    Used by the warp-parallel kernel: it materializes the full score row in
-    LDS, so N_input is capped by the device's per-workgroup LDS limit.  Beyond
-    that we skip cleanly and the benchmark records the config as
-    'design-limited'.  Also raised for a dim the MFMA kernels are not built
-    for (they are built for D = 768).
+    Two cases: the wave-per-latent rung keeps a whole score row (4 bytes per
+    key) in one workgroup's LDS, so N_input has a device-dependent ceiling;
+    and the MFMA kernels are compiled for D = 768 only.  Sweeps catch it and
+    log the point as 'design-limited' instead of failed.
     """
 
 
@@ -265,13 +263,13 @@ def device_arch(device=0):
 
 
 def _max_smem_optin(device=0):
-    """Device max LDS per workgroup, in bytes (the reference's opt-in shared
-    memory limit, cuda_wrappers.py:187-194)."""
+    """LDS bytes one workgroup of ``device`` may use (160 KiB on MI355X),
+    queried through kernels.so rather than by attribute ordinal; 48 KiB if
+    the query fails."""
     try:
-        _, lds = device_info(device)
+        return device_info(device)[1] or 48 * 1024
     except RuntimeError:
-        return 48 * 1024  # conservative default, as the reference
-    return lds if lds > 0 else 48 * 1024
+        return 48 * 1024
 
 
 def warp_smem_bytes(N_input):
@@ -284,101 +282,114 @@ def _require_dim(D, what):
         raise DesignLimited(f"{what} is built for D={D_MODEL} (got D={D})")
 
 
-def _allocate_gpu_memory(size_bytes):
-    """Allocate GPU memory."""
-    ptr = ctypes.c_void_p()
-    err = cudart.cudaMalloc(ctypes.byref(ptr), max(int(size_bytes), 1))
+def _require_warp_lds(N_input):
+    """The wave-per-latent rung's LDS ceiling, checked before any allocation."""
+    need, have = warp_smem_bytes(N_input), _max_smem_optin()
+    if need > have:
+        raise DesignLimited(
+            f"wave-per-latent rung: a {N_input}-key score row takes {need} B of LDS, "
+            f"over the {have} B a workgroup may use here (the tiled and MFMA kernels "
+            f"stream keys instead)")
+
+
+def _hip_check(err, what):
     if err != 0:
-        raise RuntimeError(f"hipMalloc failed with error {err}")
-    return ptr
+        name = cudart.hipGetErrorString(err)
+        name = name.decode(errors="replace") if name else "?"
+        raise RuntimeError(f"{what}: HIP error {err} ({name})")
 
 
-def _copy_to_gpu(host_data, gpu_ptr, size_bytes):
-    """Copy data from host to GPU."""
-    if size_bytes == 0:
-        return
-    host_ptr = host_data.ctypes.data_as(ctypes.c_void_p)
-    err = cudart.cudaMemcpy(gpu_ptr, host_ptr, size_bytes, cudaMemcpyHostToDevice)
-    if err != 0:
-        raise RuntimeError(f"hipMemcpy H2D failed with error {err}")
+# ---------------------------------------------------------------------------
+# Device memory
+# ---------------------------------------------------------------------------
+
+class DeviceBuffer:
+    """A block of device memory from hipMalloc, released by ``close()`` or on
+    leaving a ``with`` block.  ``ptr`` is the ``void*`` the 16-bit launchers
+    take, ``f32`` the ``float*`` view the fp32 ones take."""
+
+    def __init__(self, nbytes):
+        self.nbytes = int(nbytes)
+        self.ptr = ctypes.c_void_p()
+        _hip_check(cudart.hipMalloc(ctypes.byref(self.ptr), max(self.nbytes, 1)),
+                   f"hipMalloc({self.nbytes})")
+
+    @classmethod
+    def holding(cls, host):
+        """A new buffer with a copy of the contiguous host array ``host``."""
+        buf = cls(host.nbytes)
+        try:
+            buf.upload(host)
+        except Exception:
+            buf.close()
+            raise
+        return buf
+
+    @property
+    def f32(self):
+        return ctypes.cast(self.ptr, _F)
+
+    def upload(self, host):
+        host = np.ascontiguousarray(host)
+        if host.nbytes > self.nbytes:
+            raise ValueError(f"{host.nbytes} B do not fit a {self.nbytes} B buffer")
+        if host.nbytes:
+            _hip_check(cudart.hipMemcpy(self.ptr, host.ctypes.data_as(_P), host.nbytes,
+                                        cudaMemcpyHostToDevice), "host -> device copy")
+
+    def download(self, shape, dtype=np.float32):
+        """A fresh host array of ``shape`` filled from the start of the buffer."""
+        host = np.empty(shape, dtype)
+        if host.nbytes > self.nbytes:
+            raise ValueError(f"{host.nbytes} B exceed the {self.nbytes} B buffer")
+        if host.nbytes:
+            _hip_check(cudart.hipMemcpy(host.ctypes.data_as(_P), self.ptr, host.nbytes,
+                                        cudaMemcpyDeviceToHost), "device -> host copy")
+        return host
+
+    def zero(self):
+        _hip_check(cudart.hipMemset(self.ptr, 0, max(self.nbytes, 1)), "hipMemset")
+        return self
+
+    def close(self):
+        if self.ptr:
+            cudart.hipFree(self.ptr)
+            self.ptr = ctypes.c_void_p()
+
+    def __enter__(self):
+        return self
+
+    def __exit__(self, *exc):
+        self.close()
 
 
-def _copy_from_gpu(gpu_ptr, host_data, size_bytes):
-    """Copy data from GPU to host."""
-    if size_bytes == 0:
-        return
-    host_ptr = host_data.ctypes.data_as(ctypes.c_void_p)
-    err = cudart.cudaMemcpy(host_ptr, gpu_ptr, size_bytes, cudaMemcpyDeviceToHost)
-    if err != 0:
-        raise RuntimeError(f"hipMemcpy D2H failed with error {err}")
+_NULL_STREAM = ctypes.c_void_p(0)
 
 
-def _free_gpu_memory(ptr):
-    """Free GPU memory."""
-    cudart.cudaFree(ptr)
-
-
-def _fptr(p):
-    return ctypes.cast(p, ctypes.POINTER(ctypes.c_float))
-
-
-def _check_after_launch(what):
+def _raise_launch_errors(what):
+    """Refusals recorded by kernels.so, then the runtime's own launch error."""
     _lib_error_check(what)
-    err = cudart.cudaGetLastError()
+    err = cudart.hipGetLastError()
     if err != 0:
-        raise RuntimeError(f"Kernel launch failed with HIP error {err}. "
-                           f"This usually indicates a kernel configuration problem, "
-                           f"invalid memory access, or architecture incompatibility.")
+        _hip_check(err, f"{what}: launch")
 
 
 def _run_kernel(kernel_func, Q, K, V, batch_size, N_latent, N_input, D):
-    """Helper function to run a kernel with batch support (alloc, copy,
-    launch, sync, copy back, free; cuda_wrappers.py:228-289)."""
-
-    Q = np.ascontiguousarray(Q, dtype=np.float32)
-    K = np.ascontiguousarray(K, dtype=np.float32)
-    V = np.ascontiguousarray(V, dtype=np.float32)
-
-    Q_size = Q.size * 4
-    K_size = K.size * 4
-    V_size = V.size * 4
-    output_size = batch_size * N_latent * D * 4
-
-    Q_gpu = _allocate_gpu_memory(Q_size)
-    K_gpu = _allocate_gpu_memory(K_size)
-    V_gpu = _allocate_gpu_memory(V_size)
-    output_gpu = _allocate_gpu_memory(output_size)
-
-    try:
-        err = cudart.cudaMemset(output_gpu, 0, max(output_size, 1))
-        if err != 0:
-            raise RuntimeError(f"hipMemset failed with error {err}")
-
-        _copy_to_gpu(Q, Q_gpu, Q_size)
-        _copy_to_gpu(K, K_gpu, K_size)
-        _copy_to_gpu(V, V_gpu, V_size)
-
-        kernel_func(_fptr(Q_gpu), _fptr(K_gpu), _fptr(V_gpu), _fptr(output_gpu),
-                    batch_size, N_latent, N_input, D, ctypes.c_void_p(0))
-
-        _check_after_launch(getattr(kernel_func, "__name__", "kernel"))
-
-        err = cudart.cudaDeviceSynchronize()
-        if err != 0:
-            err_detail = cudart.cudaGetLastError()
-            raise RuntimeError(f"[ERROR] hipDeviceSynchronize failed with error {err}, "
-                               f"last HIP error: {err_detail}. "
-                               f"This usually indicates a kernel execution error, "
-                               f"such as invalid memory access or illegal instruction.")
-
-        output = np.zeros((batch_size, N_latent, D), dtype=np.float32)
-        _copy_from_gpu(output_gpu, output, output_size)
-        return output
-    finally:
-        _free_gpu_memory(Q_gpu)
-        _free_gpu_memory(K_gpu)
-        _free_gpu_memory(V_gpu)
-        _free_gpu_memory(output_gpu)
+    """One self-contained call of an fp32 launcher, in the manner of the
+    reference's legacy drivers (cuda_wrappers.py:228-289): device buffers are
+    made and filled, the launch runs on the null stream and is waited for,
+    and the output comes back as a new [batch_size, N_latent, D] array.
+    Every step's cost (allocation, PCIe copies) is part of the call."""
+    name = getattr(kernel_func, "__name__", "launch")
+    host = [np.ascontiguousarray(a, dtype=np.float32) for a in (Q, K, V)]
+    with contextlib.ExitStack() as owned:
+        q, k, v = (owned.enter_context(DeviceBuffer.holding(a)) for a in host)
+        out = owned.enter_context(DeviceBuffer(batch_size * N_latent * D * 4)).zero()
+        kernel_func(q.f32, k.f32, v.f32, out.f32, batch_size, N_latent, N_input, D,
+                    _NULL_STREAM)
+        _raise_launch_errors(name)
+        _hip_check(cudart.hipDeviceSynchronize(), f"{name}: waiting for the kernel")
+        return out.download((batch_size, N_latent, D))
 
 
 def _batchify(Q, K, V):
@@ -390,37 +401,27 @@ def _batchify(Q, K, V):
 
 
 def run_naive_kernel(Q, K, V, N_latent, N_input, D):
-    """Run the naive kernel (baseline - one thread per output element)."""
+    """Thread-per-output rung; 2-D or batched 3-D inputs."""
     batch_size, Q, K, V = _batchify(Q, K, V)
     return _run_kernel(lib.launch_naive_kernel, Q, K, V, batch_size, N_latent, N_input, D)
 
 
 def run_warp_parallel_kernel(Q, K, V, N_latent, N_input, D):
-    """Run the wave-per-latent kernel.
-
-    Raises DesignLimited when N_input exceeds what fits in the device's
-    per-workgroup LDS -- the kernel materializes the full score row, so this
-    is a hard design limit, not a failure.
-    """
-    needed = warp_smem_bytes(N_input)
-    avail = _max_smem_optin()
-    if needed > avail:
-        raise DesignLimited(
-            f"warp kernel needs {needed/1024:.1f} KB LDS for "
-            f"N_input={N_input} but device allows {avail/1024:.1f} KB/block "
-            f"(materializes full score row; use tiled/vectorized instead)")
+    """Wave-per-latent rung (score row in LDS); DesignLimited past its LDS
+    ceiling."""
+    _require_warp_lds(N_input)
     batch_size, Q, K, V = _batchify(Q, K, V)
     return _run_kernel(lib.launch_parallel_kernel, Q, K, V, batch_size, N_latent, N_input, D)
 
 
 def run_tiled_kernel(Q, K, V, N_latent, N_input, D):
-    """Run the tiled kernel (LDS tiling + online softmax)."""
+    """LDS-tiled online-softmax rung."""
     batch_size, Q, K, V = _batchify(Q, K, V)
     return _run_kernel(lib.launch_tiled_kernel, Q, K, V, batch_size, N_latent, N_input, D)
 
 
 def run_vectorized_kernel(Q, K, V, N_latent, N_input, D):
-    """Run the fast fp32 kernel (fp32 MFMA, online softmax)."""
+    """The fp32 MFMA kernel behind launch_optimized_kernel."""
     _require_dim(D, "the MFMA kernel")
     batch_size, Q, K, V = _batchify(Q, K, V)
     return _run_kernel(lib.launch_optimized_kernel, Q, K, V, batch_size, N_latent, N_input, D)
@@ -435,212 +436,180 @@ LAUNCHERS = {
 
 
 def _prep(arr, batch_size):
-    """Normalize Q/K/V to a contiguous fp32 [batch_size, n, D] array."""
-    arr = np.ascontiguousarray(arr, dtype=np.float32)
-    if arr.ndim == 2:
-        arr = arr[None]
-    if arr.shape[0] == 1 and batch_size > 1:
-        arr = np.repeat(arr, batch_size, axis=0)
-    return np.ascontiguousarray(arr, dtype=np.float32)
+    """``arr`` as a C-contiguous float32 [batch_size, rows, D] array: a 2-D
+    matrix gains a batch axis, and a batch of one is copied out to
+    ``batch_size`` identical batch elements."""
+    a = np.asarray(arr, dtype=np.float32)
+    if a.ndim == 2:
+        a = a.reshape((1,) + a.shape)
+    if a.shape[0] == 1 and batch_size > 1:
+        a = np.broadcast_to(a, (batch_size,) + a.shape[1:])
+    return np.ascontiguousarray(a)
 
 
-class _Events:
-    def __init__(self):
-        self.start = ctypes.c_void_p()
-        self.stop = ctypes.c_void_p()
-        cudart.cudaEventCreate(ctypes.byref(self.start))
-        cudart.cudaEventCreate(ctypes.byref(self.stop))
+# ---------------------------------------------------------------------------
+# Event timing of resident data
+# ---------------------------------------------------------------------------
 
-    def time(self, launch, iters, stream=None):
-        stream = stream if stream is not None else ctypes.c_void_p(0)
-        times = []
-        ms = ctypes.c_float(0.0)
+def _time_resident(launch, warmup, iters, label, stream=_NULL_STREAM):
+    """Warm up, then time ``iters`` launches one by one with a pair of HIP
+    events around each (record, launch, record, wait): the protocol of the
+    reference's event drivers (cuda_wrappers.py:422-446).  The first launch
+    is checked for a library refusal before any timing.  Returns the
+    per-launch times in ms."""
+    launch()
+    _lib_error_check(label)
+    for _ in range(max(warmup - 1, 0)):
+        launch()
+    err = cudart.hipDeviceSynchronize()
+    if err != 0:
+        _hip_check(cudart.hipGetLastError() or err, f"{label}: warmup")
+    start, stop = ctypes.c_void_p(), ctypes.c_void_p()
+    _hip_check(cudart.hipEventCreate(ctypes.byref(start)), "hipEventCreate")
+    _hip_check(cudart.hipEventCreate(ctypes.byref(stop)), "hipEventCreate")
+    try:
+        out, ms = [], ctypes.c_float(0.0)
         for _ in range(iters):
-            cudart.cudaEventRecord(self.start, stream)
+            cudart.hipEventRecord(start, stream)
             launch()
-            cudart.cudaEventRecord(self.stop, stream)
-            cudart.cudaEventSynchronize(self.stop)
-            cudart.cudaEventElapsedTime(ctypes.byref(ms), self.start, self.stop)
-            times.append(ms.value)
-        return times
+            cudart.hipEventRecord(stop, stream)
+            cudart.hipEventSynchronize(stop)
+            cudart.hipEventElapsedTime(ctypes.byref(ms), start, stop)
+            out.append(ms.value)
+        return out
+    finally:
+        cudart.hipEventDestroy(start)
+        cudart.hipEventDestroy(stop)
 
-    def destroy(self):
-        cudart.cudaEventDestroy(self.start)
-        cudart.cudaEventDestroy(self.stop)
 
-
-def _stats(times):
+def _mean_pstdev(times):
     if not times:
         return 0.0, 0.0
     return statistics.mean(times), (statistics.pstdev(times) if len(times) > 1 else 0.0)
 
 
-def _warmup(launch, warmup, what):
-    launch()
-    _lib_error_check(what)
-    for _ in range(max(warmup - 1, 0)):
-        launch()
-    if cudart.cudaDeviceSynchronize() != 0:
-        raise RuntimeError(f"{what} failed during warmup (HIP error "
-                           f"{cudart.cudaGetLastError()})")
+def _resident_run(launch_fn, inputs, out_shape, warmup, iters, label, scratch=(),
+                  keep_scratch=False):
+    """Shared body of the event drivers.  ``inputs`` are host arrays in the
+    launcher's element type; ``scratch`` lists the shapes of extra float32
+    device buffers (split partials).  ``launch_fn(bufs, out, scratch_bufs)``
+    issues one launch.  Returns (output, mean_ms, std_ms, host copies of the
+    scratch buffers after the last launch, or None)."""
+    with contextlib.ExitStack() as owned:
+        bufs = [owned.enter_context(DeviceBuffer.holding(a)) for a in inputs]
+        out = owned.enter_context(DeviceBuffer(int(np.prod(out_shape)) * 4)).zero()
+        sc = [owned.enter_context(DeviceBuffer(int(np.prod(s)) * 4)) for s in scratch]
+        times = _time_resident(lambda: launch_fn(bufs, out, sc), warmup, iters, label)
+        mean_ms, std_ms = _mean_pstdev(times)
+        kept = [b.download(s) for b, s in zip(sc, scratch)] if keep_scratch else None
+        return out.download(out_shape), mean_ms, std_ms, kept
 
 
 def benchmark_kernel_events(impl, Q, K, V, batch_size, N_latent, N_input, D,
                             warmup=20, iters=100):
-    """Kernel-only GPU timing via HIP events.
+    """Time launcher ``impl`` (a LAUNCHERS key) with Q/K/V already in HBM.
 
-    Allocates device buffers and copies Q/K/V to the GPU ONCE, then times only
-    the kernel launches with the data resident.  Returns (output, mean_ms,
-    std_ms).  Raises DesignLimited for the warp kernel when N_input exceeds
-    the device's per-workgroup LDS, and for the MFMA kernel when D != 768.
+    Inputs are copied to the device once; only the launches are timed, with
+    HIP events.  Returns (output [batch_size, N_latent, D], mean_ms, std_ms).
+    DesignLimited: the wave-per-latent rung past its LDS ceiling, or D != 768
+    for the MFMA kernel -- raised before anything is allocated.
     """
     if impl == 'warp':
-        needed = warp_smem_bytes(N_input)
-        avail = _max_smem_optin()
-        if needed > avail:
-            raise DesignLimited(
-                f"warp needs {needed/1024:.1f} KB LDS for "
-                f"N_input={N_input}, device allows {avail/1024:.1f} KB/block")
+        _require_warp_lds(N_input)
     if impl == 'vectorized':
         _require_dim(D, "the MFMA kernel")
     launch_fn = LAUNCHERS[impl]
+    inputs = [_prep(a, batch_size) for a in (Q, K, V)]
 
-    Q = _prep(Q, batch_size)
-    K = _prep(K, batch_size)
-    V = _prep(V, batch_size)
+    def one(bufs, out, _):
+        launch_fn(bufs[0].f32, bufs[1].f32, bufs[2].f32, out.f32, batch_size, N_latent,
+                  N_input, D, _NULL_STREAM)
 
-    Q_size, K_size, V_size = Q.size * 4, K.size * 4, V.size * 4
-    out_size = batch_size * N_latent * D * 4
-
-    Q_gpu = _allocate_gpu_memory(Q_size)
-    K_gpu = _allocate_gpu_memory(K_size)
-    V_gpu = _allocate_gpu_memory(V_size)
-    out_gpu = _allocate_gpu_memory(out_size)
-    ev = _Events()
-
-    try:
-        cudart.cudaMemset(out_gpu, 0, max(out_size, 1))
-        _copy_to_gpu(Q, Q_gpu, Q_size)
-        _copy_to_gpu(K, K_gpu, K_size)
-        _copy_to_gpu(V, V_gpu, V_size)
-
-        qp, kp, vp, op = _fptr(Q_gpu), _fptr(K_gpu), _fptr(V_gpu), _fptr(out_gpu)
-        null_stream = ctypes.c_void_p(0)
-
-        def _launch():
-            launch_fn(qp, kp, vp, op, batch_size, N_latent, N_input, D, null_stream)
-
-        _warmup(_launch, warmup, f"kernel '{impl}' (N_input={N_input}, N_latent={N_latent})")
-        times = ev.time(_launch, iters, null_stream)
-
-        output = np.zeros((batch_size, N_latent, D), dtype=np.float32)
-        _copy_from_gpu(out_gpu, output, out_size)
-        mean_ms, std_ms = _stats(times)
-        return output, mean_ms, std_ms
-    finally:
-        ev.destroy()
-        _free_gpu_memory(Q_gpu)
-        _free_gpu_memory(K_gpu)
-        _free_gpu_memory(V_gpu)
-        _free_gpu_memory(out_gpu)
+    out, mean_ms, std_ms, _ = _resident_run(
+        one, inputs, (batch_size, N_latent, D), warmup, iters,
+        f"kernel '{impl}' (N_latent={N_latent}, N_input={N_input})")
+    return out, mean_ms, std_ms
 
 
 def choose_num_splits(N_latent, N_input, batch_size, sm_count=142,
                       latents_per_block=4):
-    """Pick num_splits so the partial-kernel grid oversubscribes the GPU.
-
-    Base workgroups (no split) = ceil(Nl/latents_per_block)*batch.  Aim for
-    ~4x sm_count workgroups, capped so each split still holds >= ~16 keys
-    (cuda_wrappers.py:456-467).  On MI355X pass sm_count=256 (compute units;
-    see ``device_info``).
+    """The reference's split heuristic, unchanged (cuda_wrappers.py:456-467):
+    enough splits for about four workgroups of ``latents_per_block`` latents
+    per compute unit, with at least 16 keys per split.  The reference's
+    split-K drivers use it with latents_per_block = 4 (fp32) and 16 (fp16)
+    when num_splits is None; ``sm_count`` 142 is its L40S default (MI355X
+    has 256 compute units, see ``device_info``).
     """
     base = math.ceil(N_latent / latents_per_block) * batch_size
     target = max(1, (4 * sm_count) // max(1, base))
     return max(1, min(N_input // 16, target)) or 1
 
 
-def _splitk_run(launch, Qd, Kd, Vd, batch_size, N_latent, N_input, D, num_splits,
-                warmup, iters, what, keep_partials=False):
-    """Shared body of the split-K event drivers: Qd/Kd/Vd are host arrays in
-    the element type the launcher takes; scratch po/pm/pl is allocated once."""
-    out_size = batch_size * N_latent * D * 4
-    po_size = batch_size * N_latent * num_splits * D * 4
-    pml_size = batch_size * N_latent * num_splits * 4
+def _default_splits(num_splits, N_latent, N_input, batch_size, sm_count, latents_per_block,
+                    keys_per_tile):
+    """num_splits of a split-K driver: None -> the reference's default,
+    choose_num_splits (cuda_wrappers.py:480-481, 553-555); "plan" -> the
+    library's cost-model plan (plan_num_splits); an int is used as given."""
+    if num_splits is None:
+        return choose_num_splits(N_latent, N_input, batch_size, sm_count, latents_per_block)
+    if isinstance(num_splits, str):
+        if num_splits != "plan":
+            raise ValueError(f"num_splits must be an int, None or 'plan' (got {num_splits!r})")
+        return plan_num_splits(N_latent, N_input, batch_size, sm_count, keys_per_tile)
+    return int(num_splits)
 
-    Q_gpu = _allocate_gpu_memory(Qd.nbytes)
-    K_gpu = _allocate_gpu_memory(Kd.nbytes)
-    V_gpu = _allocate_gpu_memory(Vd.nbytes)
-    out_gpu = _allocate_gpu_memory(out_size)
-    po_gpu = _allocate_gpu_memory(po_size)
-    pm_gpu = _allocate_gpu_memory(pml_size)
-    pl_gpu = _allocate_gpu_memory(pml_size)
-    ev = _Events()
-    try:
-        cudart.cudaMemset(out_gpu, 0, max(out_size, 1))
-        _copy_to_gpu(Qd, Q_gpu, Qd.nbytes)
-        _copy_to_gpu(Kd, K_gpu, Kd.nbytes)
-        _copy_to_gpu(Vd, V_gpu, Vd.nbytes)
-        null_stream = ctypes.c_void_p(0)
 
-        def _launch():
-            launch(Q_gpu, K_gpu, V_gpu, _fptr(out_gpu), _fptr(po_gpu), _fptr(pm_gpu),
-                   _fptr(pl_gpu), batch_size, N_latent, N_input, D, num_splits, null_stream)
+def _splitk_run(launch, inputs, batch_size, N_latent, N_input, D, num_splits, warmup, iters,
+                what, keep_partials=False):
+    """Event-time a split-K launcher whose caller-owned scratch (po, pm, pl)
+    is allocated once.  ``launch`` takes the launcher's argument list with
+    Q, K, V as DeviceBuffers.  Returns (output, mean_ms, std_ms) and, with
+    ``keep_partials``, host copies of the (po, pm, pl) the last launch wrote."""
+    rows = (batch_size, N_latent, num_splits)
 
-        _warmup(_launch, warmup,
-                f"{what} (Nl={N_latent} Ni={N_input} splits={num_splits})")
-        times = ev.time(_launch, iters, null_stream)
+    def one(bufs, out, sc):
+        launch(bufs[0], bufs[1], bufs[2], out.f32, sc[0].f32, sc[1].f32, sc[2].f32,
+               batch_size, N_latent, N_input, D, num_splits, _NULL_STREAM)
 
-        output = np.zeros((batch_size, N_latent, D), dtype=np.float32)
-        _copy_from_gpu(out_gpu, output, out_size)
-        mean_ms, std_ms = _stats(times)
-        if keep_partials:
-            po = np.zeros((batch_size, N_latent, num_splits, D), np.float32)
-            pm = np.zeros((batch_size, N_latent, num_splits), np.float32)
-            pl = np.zeros((batch_size, N_latent, num_splits), np.float32)
-            _copy_from_gpu(po_gpu, po, po_size)
-            _copy_from_gpu(pm_gpu, pm, pml_size)
-            _copy_from_gpu(pl_gpu, pl, pml_size)
-            return output, mean_ms, std_ms, (po, pm, pl)
-        return output, mean_ms, std_ms
-    finally:
-        ev.destroy()
-        for p in (Q_gpu, K_gpu, V_gpu, out_gpu, po_gpu, pm_gpu, pl_gpu):
-            _free_gpu_memory(p)
+    out, mean_ms, std_ms, kept = _resident_run(
+        one, inputs, (batch_size, N_latent, D), warmup, iters,
+        f"{what} (N_latent={N_latent} N_input={N_input} splits={num_splits})",
+        scratch=(rows + (D,), rows, rows), keep_scratch=keep_partials)
+    if not keep_partials:
+        return out, mean_ms, std_ms
+    return out, mean_ms, std_ms, tuple(kept)
 
 
 def benchmark_splitk_events(Q, K, V, batch_size, N_latent, N_input, D,
                             warmup=20, iters=100, num_splits=None, sm_count=142):
-    """HIP-event timing for the split-K (key-parallel) kernel.
+    """Event timing of launch_splitk_kernel (partials + LSE merge).
 
-    Allocates Q/K/V/out AND the partial scratch (po/pm/pl) once, then times the
-    partial+combine launches.  Returns (output, mean_ms, std_ms, num_splits).
+    The split scratch is allocated once with the inputs.  num_splits: None
+    takes the reference's choose_num_splits(..., sm_count) with 4-latent
+    blocks, "plan" the library's plan for ``sm_count`` compute units.
+    Returns (output, mean_ms, std_ms, num_splits).
     """
     if not HAS_SPLITK:
-        raise RuntimeError("kernels.so has no launch_splitk_kernel (rebuild "
-                           "with csrc/xattn_flash_f32.hip).")
+        raise RuntimeError("this kernels.so does not export launch_splitk_kernel")
     _require_dim(D, "split-K")
-    if num_splits is None:
-        num_splits = plan_num_splits(N_latent, N_input, batch_size, sm_count)
-    Q = _prep(Q, batch_size)
-    K = _prep(K, batch_size)
-    V = _prep(V, batch_size)
+    num_splits = _default_splits(num_splits, N_latent, N_input, batch_size, sm_count, 4,
+                                 KEYS_PER_TILE_F32)
+    inputs = [_prep(a, batch_size) for a in (Q, K, V)]
     launch = lambda q, k, v, *rest: lib.launch_splitk_kernel(  # noqa: E731
-        _fptr(q), _fptr(k), _fptr(v), *rest)
-    out, mean_ms, std_ms = _splitk_run(launch, Q, K, V, batch_size, N_latent, N_input, D,
+        q.f32, k.f32, v.f32, *rest)
+    out, mean_ms, std_ms = _splitk_run(launch, inputs, batch_size, N_latent, N_input, D,
                                        num_splits, warmup, iters, "split-K")
     return out, mean_ms, std_ms, num_splits
 
 
 def splitk_partials(Q, K, V, batch_size, N_latent, N_input, D, num_splits):
-    """Run launch_splitk_kernel once; return (output, (po, pm, pl)) -- the
-    caller-visible scratch the reference's split-K writes."""
+    """One launch_splitk_kernel call; returns (output, (po, pm, pl)), the
+    caller-visible scratch in the reference's layout."""
     _require_dim(D, "split-K")
-    Q = _prep(Q, batch_size)
-    K = _prep(K, batch_size)
-    V = _prep(V, batch_size)
+    inputs = [_prep(a, batch_size) for a in (Q, K, V)]
     launch = lambda q, k, v, *rest: lib.launch_splitk_kernel(  # noqa: E731
-        _fptr(q), _fptr(k), _fptr(v), *rest)
-    out, _, _, parts = _splitk_run(launch, Q, K, V, batch_size, N_latent, N_input, D,
+        q.f32, k.f32, v.f32, *rest)
+    out, _, _, parts = _splitk_run(launch, inputs, batch_size, N_latent, N_input, D,
                                    num_splits, 1, 0, "split-K", keep_partials=True)
     return out, parts
 
@@ -671,47 +640,28 @@ def _half_inputs(Q, K, V, batch_size, D, bf16):
 def _wmma_events(launch_fn, what, Q, K, V, batch_size, N_latent, N_input, D, warmup, iters,
                  bf16):
     _require_dim(D, what)
-    Qh, Kh, Vh = _half_inputs(Q, K, V, batch_size, D, bf16)
-    out_size = batch_size * N_latent * D * 4
-    Q_gpu = _allocate_gpu_memory(Qh.nbytes)
-    K_gpu = _allocate_gpu_memory(Kh.nbytes)
-    V_gpu = _allocate_gpu_memory(Vh.nbytes)
-    out_gpu = _allocate_gpu_memory(out_size)
-    ev = _Events()
-    try:
-        cudart.cudaMemset(out_gpu, 0, max(out_size, 1))
-        _copy_to_gpu(Qh, Q_gpu, Qh.nbytes)
-        _copy_to_gpu(Kh, K_gpu, Kh.nbytes)
-        _copy_to_gpu(Vh, V_gpu, Vh.nbytes)
-        op = _fptr(out_gpu)
-        null_stream = ctypes.c_void_p(0)
+    inputs = _half_inputs(Q, K, V, batch_size, D, bf16)
 
-        def _launch():
-            launch_fn(Q_gpu, K_gpu, V_gpu, op, batch_size, N_latent, N_input, D, null_stream)
+    def one(bufs, out, _):
+        launch_fn(bufs[0].ptr, bufs[1].ptr, bufs[2].ptr, out.f32, batch_size, N_latent,
+                  N_input, D, _NULL_STREAM)
 
-        _warmup(_launch, warmup, f"{what} (Nl={N_latent} Ni={N_input})")
-        times = ev.time(_launch, iters, null_stream)
-        output = np.zeros((batch_size, N_latent, D), dtype=np.float32)
-        _copy_from_gpu(out_gpu, output, out_size)
-        mean_ms, std_ms = _stats(times)
-        return output, mean_ms, std_ms
-    finally:
-        ev.destroy()
-        for p in (Q_gpu, K_gpu, V_gpu, out_gpu):
-            _free_gpu_memory(p)
+    out, mean_ms, std_ms, _ = _resident_run(
+        one, inputs, (batch_size, N_latent, D), warmup, iters,
+        f"{what} (N_latent={N_latent} N_input={N_input})")
+    return out, mean_ms, std_ms
 
 
 def benchmark_wmma_events(Q, K, V, batch_size, N_latent, N_input, D,
                           warmup=20, iters=100):
-    """HIP-event timing for the fp16 MFMA kernel.
+    """Event timing of launch_wmma_kernel (fp16 MFMA, fp32 accumulate).
 
-    Takes fp32 Q/K/V (same references the other kernels use), pre-scales Q by
-    1/sqrt(D), casts to fp16, runs the MFMA kernel, and returns (fp32 output,
-    mean_ms, std_ms).
+    fp32 Q/K/V in, as for the other drivers; Q is scaled by 1/sqrt(D) and all
+    three are rounded to fp16 on the host.  Returns (fp32 output, mean_ms,
+    std_ms).
     """
     if not HAS_WMMA:
-        raise RuntimeError("kernels.so has no launch_wmma_kernel (rebuild with "
-                           "csrc/xattn_flash_f16.hip).")
+        raise RuntimeError("this kernels.so does not export launch_wmma_kernel")
     return _wmma_events(lib.launch_wmma_kernel, "fp16 MFMA kernel", Q, K, V, batch_size,
                         N_latent, N_input, D, warmup, iters, bf16=False)
 
@@ -720,7 +670,7 @@ def benchmark_wmma_bf16_events(Q, K, V, batch_size, N_latent, N_input, D,
                                warmup=20, iters=100):
     """bf16 twin of ``benchmark_wmma_events`` (additive)."""
     if not HAS_WMMA_BF16:
-        raise RuntimeError("kernels.so has no launch_wmma_bf16_kernel.")
+        raise RuntimeError("this kernels.so does not export launch_wmma_bf16_kernel")
     return _wmma_events(lib.launch_wmma_bf16_kernel, "bf16 MFMA kernel", Q, K, V, batch_size,
                         N_latent, N_input, D, warmup, iters, bf16=True)
 
@@ -728,12 +678,11 @@ def benchmark_wmma_bf16_events(Q, K, V, batch_size, N_latent, N_input, D,
 def _wmma_splitk(launch_fn, what, Q, K, V, batch_size, N_latent, N_input, D, warmup, iters,
                  num_splits, sm_count, bf16, keep_partials=False):
     _require_dim(D, what)
-    if num_splits is None:
-        num_splits = plan_num_splits(N_latent, N_input, batch_size, sm_count,
-                                     KEYS_PER_TILE_F16)
-    Qh, Kh, Vh = _half_inputs(Q, K, V, batch_size, D, bf16)
-    launch = lambda q, k, v, *rest: launch_fn(q, k, v, *rest)  # noqa: E731
-    res = _splitk_run(launch, Qh, Kh, Vh, batch_size, N_latent, N_input, D, num_splits,
+    num_splits = _default_splits(num_splits, N_latent, N_input, batch_size, sm_count, 16,
+                                 KEYS_PER_TILE_F16)
+    inputs = _half_inputs(Q, K, V, batch_size, D, bf16)
+    launch = lambda q, k, v, *rest: launch_fn(q.ptr, k.ptr, v.ptr, *rest)  # noqa: E731
+    res = _splitk_run(launch, inputs, batch_size, N_latent, N_input, D, num_splits,
                       warmup, iters, what, keep_partials=keep_partials)
     return res, num_splits
 
@@ -741,14 +690,15 @@ def _wmma_splitk(launch_fn, what, Q, K, V, batch_size, N_latent, N_input, D, war
 def benchmark_wmma_splitk_events(Q, K, V, batch_size, N_latent, N_input, D,
                                  warmup=20, iters=100, num_splits=None,
                                  sm_count=142):
-    """HIP-event timing for the fp16 MFMA split-K kernel (fp16 + key-split).
+    """Event timing of launch_wmma_splitk_kernel (fp16, key-parallel).
 
-    fp16 Q/K/V (Q pre-scaled by 1/sqrt(D)), fp32 scratch + output.  Returns
-    (fp32 output, mean_ms, std_ms, num_splits).
+    Inputs prepared as for ``benchmark_wmma_events``; fp32 scratch and
+    output.  num_splits: None takes the reference's choose_num_splits with
+    16-latent blocks, "plan" the library's plan.  Returns (fp32 output,
+    mean_ms, std_ms, num_splits).
     """
     if not HAS_WMMA_SPLITK:
-        raise RuntimeError("kernels.so has no launch_wmma_splitk_kernel "
-                           "(rebuild with csrc/xattn_flash_f16.hip).")
+        raise RuntimeError("this kernels.so does not export launch_wmma_splitk_kernel")
     (out, mean_ms, std_ms), s = _wmma_splitk(
         lib.launch_wmma_splitk_kernel, "fp16 split-K", Q, K, V, batch_size, N_latent,
         N_input, D, warmup, iters, num_splits, sm_count, bf16=False)
@@ -760,7 +710,7 @@ def benchmark_wmma_splitk_bf16_events(Q, K, V, batch_size, N_latent, N_input, D,
                                       sm_count=142):
     """bf16 twin of ``benchmark_wmma_splitk_events`` (additive)."""
     if not HAS_WMMA_SPLITK_BF16:
-        raise RuntimeError("kernels.so has no launch_wmma_splitk_bf16_kernel.")
+        raise RuntimeError("this kernels.so does not export launch_wmma_splitk_bf16_kernel")
     (out, mean_ms, std_ms), s = _wmma_splitk(
         lib.launch_wmma_splitk_bf16_kernel, "bf16 split-K", Q, K, V, batch_size, N_latent,
         N_input, D, warmup, iters, num_splits, sm_count, bf16=True)

@@ -6,8 +6,10 @@ Fused flash kernels cap the head dimension, so at D = 768 the framework
 baseline is whichever backend still accepts the shape.  Each backend is
 forced in turn at the anchor point (B = 1, N_latent = 256, N_input = 4096) in
 fp32, fp16 and bf16; a run is timed with events, a refusal is logged with
-its message.  16-bit 'math' is the spelled-out materialized product (see
-sdpa_bench.py).  Off a GPU box the script says so and exits 0.
+its message.  16-bit 'math' is not run (switched off, see sdpa_bench.py) and
+is logged as such; the hand-written materialized product (bmm_fp16 /
+bmm_bf16) is timed in its place under its own name.  Off a GPU box the
+script says so and exits 0.
 
     python experiments/e0_sdpa_backend.py
     python experiments/e0_sdpa_backend.py --n-latent 256 --n-input 4096 --csv results/e0.csv
@@ -23,6 +25,7 @@ PROBES = [
     ("sdpa_flash", "flash", ("fp16", "bf16")),
     ("sdpa_efficient", "efficient", ("fp32", "fp16", "bf16")),
     ("sdpa_math", "math", ("fp32", "fp16", "bf16")),
+    ("bmm", None, ("fp16", "bf16")),
 ]
 
 
@@ -31,18 +34,22 @@ def probe(nl, ni, warmup, iters):
     import math
 
     import torch
-    from sdpa_bench import sdpa_callable, time_events, torch_dtype
+    from sdpa_bench import (MATH_16BIT_OFF, materialized_bmm, sdpa_callable, time_events,
+                            torch_dtype)
 
     results = []
     scale = 1.0 / math.sqrt(D)
     gen = torch.Generator(device="cuda").manual_seed(0)
     for impl, backend, precisions in PROBES:
         for prec in precisions:
+            if backend == "math" and prec != "fp32":
+                results.append((impl, prec, "switched-off", None, None, MATH_16BIT_OFF[:160]))
+                continue
             dt = torch_dtype(prec)
             q = torch.randn(1, 1, nl, D, device="cuda", generator=gen).to(dt)
             k = torch.randn(1, 1, ni, D, device="cuda", generator=gen).to(dt)
             v = torch.randn(1, 1, ni, D, device="cuda", generator=gen).to(dt)
-            fn = sdpa_callable(backend, prec)
+            fn = materialized_bmm if backend is None else sdpa_callable(backend, prec)
             try:
                 fn(q, k, v, scale)
                 times = time_events(lambda: fn(q, k, v, scale), warmup, iters)

@@ -36,8 +36,8 @@ STYLE = {
     "wmma_splitk": ("#e377c2", "X", "fp16 MFMA split-K"),
     "wmma_splitk_bf16": ("#f7b6d2", "X", "bf16 MFMA split-K"),
     "sdpa_math": ("#8c564b", "v", "PyTorch SDPA-math (materialized)"),
-    "sdpa_math_fp16": ("#c49c94", "v", "PyTorch SDPA-math fp16"),
-    "sdpa_math_bf16": ("#dbb9a9", "v", "PyTorch SDPA-math bf16"),
+    "bmm_fp16": ("#c49c94", "v", "torch bmm/softmax/bmm fp16 (materialized)"),
+    "bmm_bf16": ("#dbb9a9", "v", "torch bmm/softmax/bmm bf16 (materialized)"),
     "sdpa_efficient": ("#17becf", "<", "PyTorch SDPA-efficient (fused)"),
     "sdpa_efficient_fp16": ("#9edae5", "<", "PyTorch SDPA-efficient fp16"),
     "sdpa_efficient_bf16": ("#6fc3cf", "<", "PyTorch SDPA-efficient bf16"),

@@ -9,9 +9,13 @@ Implementations (the reference's names, experiments/bench_perceiver_ni.py:
     splitk                        fp32 split-K   benchmark_splitk_events
     wmma wmma_splitk              fp16 MFMA      benchmark_wmma[_splitk]_events
     wmma_bf16 wmma_splitk_bf16    bf16 MFMA      benchmark_wmma[_splitk]_bf16_events
-    sdpa_math sdpa_efficient sdpa_flash  (fp32; suffix _fp16 or _bf16 for 16 bit)
+    sdpa_math sdpa_efficient sdpa_flash  (fp32; suffix _fp16 or _bf16 for 16 bit;
+                                  16-bit sdpa_math is switched off and logs an error)
+    bmm_fp16 bmm_bf16             materialized bmm/softmax/bmm with a contiguous
+                                  K^T (the 16-bit materialized baseline; not SDPA)
 
-The split drivers plan their split count for the device's own CU count.
+The split drivers take the library's planned split count for the device's
+own CU count (num_splits="plan"), not the reference's choose_num_splits default.
 """
 
 import numpy as np
@@ -44,7 +48,8 @@ def run_impl(cw, impl, Q, K, V, B, nl, ni, warmup, iters, cu_count):
                                                           warmup, iters)
     elif impl == "splitk":
         out, mean_ms, std_ms, s = cw.benchmark_splitk_events(Q, K, V, B, nl, ni, D, warmup,
-                                                             iters, sm_count=cu_count)
+                                                             iters, num_splits="plan",
+                                                             sm_count=cu_count)
         note = f"splits={s}"
     elif impl == "wmma":
         out, mean_ms, std_ms = cw.benchmark_wmma_events(Q, K, V, B, nl, ni, D, warmup, iters)
@@ -54,8 +59,14 @@ def run_impl(cw, impl, Q, K, V, B, nl, ni, warmup, iters, cu_count):
     elif impl in ("wmma_splitk", "wmma_splitk_bf16"):
         fn = (cw.benchmark_wmma_splitk_bf16_events if impl.endswith("bf16")
               else cw.benchmark_wmma_splitk_events)
-        out, mean_ms, std_ms, s = fn(Q, K, V, B, nl, ni, D, warmup, iters, sm_count=cu_count)
+        out, mean_ms, std_ms, s = fn(Q, K, V, B, nl, ni, D, warmup, iters, num_splits="plan",
+                                     sm_count=cu_count)
         note = f"splits={s}"
+    elif impl in ("bmm_fp16", "bmm_bf16"):
+        from sdpa_bench import benchmark_bmm_events
+        out, mean_ms, std_ms = benchmark_bmm_events(Q, K, V, B, nl, ni, D, precision_of(impl),
+                                                    warmup, iters)
+        note = "bmm(Q, K^T contiguous) / softmax / bmm"
     elif impl.startswith("sdpa_"):
         from sdpa_bench import benchmark_sdpa_events
         backend, prec = sdpa_backend_of(impl), precision_of(impl)
@@ -96,7 +107,7 @@ def measure(cw, experiment, gpu, impl, Q, K, V, ref, B, nl, ni, warmup, iters, c
         row.update(status="error", note=(str(e).splitlines() or [repr(e)])[0][:120])
         return row
     max_abs, rel = errors(out, ref, nl)
-    materialized = impl.startswith("sdpa_math")
+    materialized = impl.startswith("sdpa_math") or impl.startswith("bmm_")
     out_prec = "fp32" if impl.startswith("wmma") else None
     rl = roofline.roofline_row(B, nl, ni, D, mean_ms / 1e3, gpu, prec,
                                materialized=materialized, out_precision=out_prec)

@@ -138,6 +138,25 @@ def test_wmma_plan(cw):
             assert split(b, nl, ni, s, 256) == lpw
 
 
+def test_split_drivers_default_to_the_reference_heuristic(cw):
+    """num_splits=None in the split-K drivers means what it means in the
+    reference (cuda_wrappers.py:480-481, 553-555): choose_num_splits with
+    4-latent blocks for fp32 and 16-latent blocks for fp16, at the caller's
+    sm_count (default 142).  "plan" asks for the library's own plan."""
+    d = cw._default_splits
+    f32, f16 = cw.KEYS_PER_TILE_F32, cw.KEYS_PER_TILE_F16
+    assert d(None, 256, 4096, 1, 142, 4, f32) == 8
+    assert d(None, 256, 4096, 1, 256, 4, f32) == 16
+    assert d(None, 256, 4096, 1, 142, 16, f16) == 35
+    assert d(None, 256, 4096, 1, 256, 16, f16) == 64
+    assert d(None, 1024, 784, 32, 142, 4, f32) == 1
+    assert d(7, 256, 4096, 1, 142, 4, f32) == 7
+    assert d("plan", 256, 4096, 1, 256, 4, f32) == cw.f32_plan(1, 256, 4096, 256)[1]
+    assert d("plan", 256, 4096, 1, 256, 16, f16) == cw.wmma_plan(1, 256, 4096, 256)[1]
+    with pytest.raises(ValueError):
+        d("auto", 256, 4096, 1, 256, 4, f32)
+
+
 def test_choose_num_splits_known_values(cw):
     # values worked out by hand from cuda_wrappers.py:456-467
     assert cw.choose_num_splits(256, 4096, 1) == 8            # sm 142, lpb 4

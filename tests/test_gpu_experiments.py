@@ -88,21 +88,25 @@ def test_sdpa_math_matches_oracle(oracle):
     out, mean_ms, _ = benchmark_sdpa_events(q, k, v, 2, 24, 70, 768, "math", "fp32", 1, 2)
     assert out.shape == (2, 24, 768) and mean_ms > 0
     assert oracle.rel_err(out, ref) < 1e-5
-    # the spelled-out 16-bit materialized product
+    # the hand-written 16-bit materialized product; 16-bit SDPA math refuses
+    from sdpa_bench import benchmark_bmm_events
     for prec, tol in (("fp16", 5e-3), ("bf16", 2e-2)):
-        out, _, _ = benchmark_sdpa_events(q, k, v, 2, 24, 70, 768, "math", prec, 1, 2)
+        out, _, _ = benchmark_bmm_events(q, k, v, 2, 24, 70, 768, prec, 1, 2)
         assert np.all(np.isfinite(out)) and oracle.rel_err(out, ref) < tol, prec
+        with pytest.raises(RuntimeError, match="switched off"):
+            benchmark_sdpa_events(q, k, v, 2, 24, 70, 768, "math", prec, 1, 2)
 
 
 def test_sdpa_backend_probe_runs_math():
     import e0_sdpa_backend
     res = e0_sdpa_backend.probe(16, 64, 1, 2)
-    assert len(res) == 8
+    assert len(res) == 10
     by = {(impl, prec): (status, note) for impl, prec, status, _, _, note in res}
     assert by[("sdpa_math", "fp32")][0] == "ok"
-    assert by[("sdpa_math", "bf16")][0] == "ok"
+    assert by[("sdpa_math", "bf16")][0] == "switched-off"
+    assert by[("bmm", "bf16")][0] == "ok" and by[("bmm", "fp16")][0] == "ok"
     for status, note in by.values():
-        assert status in ("ok", "unsupported") and (status == "ok" or note)
+        assert status in ("ok", "unsupported", "switched-off") and (status == "ok" or note)
 
 
 def test_anchor_comparison_table(tmp_path, monkeypatch, cw):

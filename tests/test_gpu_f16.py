@@ -60,6 +60,26 @@ def test_shapes(cw, oracle, bf16, b, nl, ni):
 
 
 @pytest.mark.parametrize("bf16", [False, True], ids=["fp16", "bf16"])
+@pytest.mark.parametrize("b,nl,ni,s", [(16, 512, 784, 0), (1, 64, 784, 0), (2, 48, 500, 9)],
+                         ids=["config5", "split-plan", "splitk-9"])
+def test_bitwise_repeatable(cw, oracle, bf16, b, nl, ni, s):
+    """Two runs on the same inputs give identical bits: no reduction order
+    depends on timing (the two owners of a latent block, the split partials
+    and their merge are combined in a fixed order).  s = 0: the plain entry
+    point with the library's own plan; s > 0: the split-K entry point."""
+    q, k, v = oracle.make_inputs(b, nl, ni, 768, seed=77)
+    if s == 0:
+        a, c = _run(cw, q, k, v, bf16), _run(cw, q, k, v, bf16)
+    else:
+        a, pa = cw.wmma_splitk_partials(q, k, v, b, nl, ni, 768, s, bf16=bf16)
+        c, pc = cw.wmma_splitk_partials(q, k, v, b, nl, ni, 768, s, bf16=bf16)
+        for x, y in zip(pa, pc):
+            assert np.array_equal(x, y)
+    assert np.array_equal(a, c)
+    _check(oracle, cw, a, q, k, v, bf16)
+
+
+@pytest.mark.parametrize("bf16", [False, True], ids=["fp16", "bf16"])
 def test_empty_keys(cw, oracle, bf16):
     q, _, _ = oracle.make_inputs(1, 20, 1, 768, seed=1)
     k = np.zeros((1, 0, 768), np.float32)

@@ -1,6 +1,6 @@
-"""Seeded random shapes through every launch plan: the fp32 and bf16 entry
-points choose their workgroup size (64 / 32 / 16 latents) and key splits
-from the shape, and the split-K entry points their workgroup size from the
+"""Seeded random shapes through every launch plan: the fp32, fp16 and bf16
+entry points choose their workgroup size (64 / 32 / 16 latents) and key
+splits from the shape, and the split-K entry points their workgroup size from the
 caller's num_splits, so random (B, N_latent, N_input, num_splits) draws reach
 plans the fixed-shape tests do not.  Each output is checked against the
 float64 oracle (fp32 gate, or 2e-2 relative on the rounded 16-bit inputs)."""
@@ -41,13 +41,15 @@ def test_fp32_plans(cw, oracle, b, nl, ni, s):
     fp32_gate(out, ref)
 
 
+@pytest.mark.parametrize("bf16", [False, True], ids=["fp16", "bf16"])
 @pytest.mark.parametrize("b,nl,ni,s", SHAPES)
-def test_bf16_plans(cw, oracle, b, nl, ni, s):
+def test_16bit_plans(cw, oracle, b, nl, ni, s, bf16):
     q, k, v = oracle.make_inputs(b, nl, ni, 768, seed=b * 7919 + nl * 31 + ni + 1)
-    qh, kh, vh = cw._half_inputs(q, k, v, b, 768, True)
-    f = oracle.bf16_bits_to_f32
+    qh, kh, vh = cw._half_inputs(q, k, v, b, 768, bf16)
+    f = oracle.bf16_bits_to_f32 if bf16 else (lambda a: a.astype(np.float32))
     ref = oracle.attention_f64(f(qh).astype(np.float64) * math.sqrt(768), f(kh), f(vh))
-    out, _, _ = cw.benchmark_wmma_bf16_events(q, k, v, b, nl, ni, 768, warmup=0, iters=1)
+    run = cw.benchmark_wmma_bf16_events if bf16 else cw.benchmark_wmma_events
+    out, _, _ = run(q, k, v, b, nl, ni, 768, warmup=0, iters=1)
     assert np.all(np.isfinite(out)) and oracle.rel_err(out, ref) < 2e-2
-    out, _ = cw.wmma_splitk_partials(q, k, v, b, nl, ni, 768, min(s, ni), bf16=True)
+    out, _ = cw.wmma_splitk_partials(q, k, v, b, nl, ni, 768, min(s, ni), bf16=bf16)
     assert np.all(np.isfinite(out)) and oracle.rel_err(out, ref) < 2e-2

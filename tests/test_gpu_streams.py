@@ -26,12 +26,6 @@ def _hip(cw):
     return hip
 
 
-def _dev(cw, a):
-    p = cw._allocate_gpu_memory(a.nbytes)
-    cw._copy_to_gpu(a, p, a.nbytes)
-    return p
-
-
 @pytest.mark.parametrize("entry", ["launch_optimized_kernel", "launch_wmma_bf16_kernel"])
 def test_split_launches_on_two_streams(cw, oracle, entry):
     b, nl, ni, d = 1, 64, 784, 768
@@ -49,28 +43,27 @@ def test_split_launches_on_two_streams(cw, oracle, entry):
         for i in range(2):
             q, k, v = oracle.make_inputs(b, nl, ni, d, seed=100 + i)
             if entry == "launch_optimized_kernel":
-                ins = [_dev(cw, a) for a in (q, k, v)]
-                args = [cw._fptr(p) for p in ins]
+                ins = [cw.DeviceBuffer.holding(a) for a in (q, k, v)]
+                args = [p.f32 for p in ins]
                 refs.append(oracle.attention_f64(q, k, v))
             else:
                 host = cw._half_inputs(q, k, v, b, d, bf16=True)
-                ins = [_dev(cw, a) for a in host]
-                args = ins
+                ins = [cw.DeviceBuffer.holding(a) for a in host]
+                args = [p.ptr for p in ins]
                 f = oracle.bf16_bits_to_f32
                 refs.append(oracle.attention_f64(
                     f(host[0]).astype(np.float64) * np.sqrt(d), f(host[1]), f(host[2])))
-            out = cw._allocate_gpu_memory(b * nl * d * 4)
+            out = cw.DeviceBuffer(b * nl * d * 4)
             bufs += ins + [out]
             outs.append((args, out))
         fn = getattr(cw.lib, entry)
         for _ in range(40):
             for (args, out), s in zip(outs, streams):
-                fn(*args, cw._fptr(out), b, nl, ni, d, s)
+                fn(*args, out.f32, b, nl, ni, d, s)
         cw._lib_error_check(entry)
         assert cw.cudart.cudaDeviceSynchronize() == 0
         for (args, out), ref in zip(outs, refs):
-            got = np.empty((b, nl, d), np.float32)
-            cw._copy_from_gpu(out, got, got.nbytes)
+            got = out.download((b, nl, d))
             if entry == "launch_optimized_kernel":
                 fp32_gate(got, ref)
             else:
@@ -78,6 +71,6 @@ def test_split_launches_on_two_streams(cw, oracle, entry):
     finally:
         assert cw.cudart.cudaDeviceSynchronize() == 0
         for p in bufs:
-            cw._free_gpu_memory(p)
+            p.close()
         for s in streams:
             hip.hipStreamDestroy(s)

@@ -261,13 +261,13 @@ def _mut_wrong_axis(q, k, v):
     return np.matmul(p, v)
 
 
-def _mut_transposed_qk(q, k, v):
-    # uses K's rows against Q transposed where shapes allow: S^T instead of S
-    q = o._as3(q).astype(np.float64); k = o._as3(k).astype(np.float64)
-    v = o._as3(v).astype(np.float64)
-    s = np.matmul(q, np.swapaxes(k, 1, 2)) / math.sqrt(q.shape[-1])
-    p = scipy.special.softmax(s, axis=-1)
-    return np.matmul(p, v) + 1e-3 * np.matmul(p, v).mean()
+def _mut_k_read_transposed(q, k, v):
+    # K's [N_input, D] rows read as if the buffer held K^T ([D, N_input]
+    # row-major): the element at (j, d) is taken from flat index d * NI + j
+    k = o._as3(k).astype(np.float64)
+    b, ni, d = k.shape
+    k_wrong = k.reshape(b, d, ni).swapaxes(1, 2)
+    return o.attention_f64(q, k_wrong, v)
 
 
 def _mut_dropped_max_term(q, k, v):
@@ -292,7 +292,7 @@ def _mut_wrong_sqrt(q, k, v):
                            k, v)
 
 
-@pytest.mark.parametrize("mutant", [_mut_no_scale, _mut_wrong_axis, _mut_transposed_qk,
+@pytest.mark.parametrize("mutant", [_mut_no_scale, _mut_wrong_axis, _mut_k_read_transposed,
                                     _mut_dropped_max_term, _mut_wrong_sqrt],
                          ids=lambda f: f.__name__)
 def test_planted_mistakes_are_caught(mutant):
@@ -309,15 +309,21 @@ def test_planted_merge_mistakes_are_caught():
     q, k, v = _rand(1, 3, 40, 16, 1)
     po, pm, pl = o.splitk_partials(q, k, v, 4)
     ref = o.attention_f64(q, k, v)
-    # forgetting the exp(pm - M) weights, or the sentinel skip, must be visible
+    assert np.allclose(o.splitk_combine(po, pm, pl, eps=0.0), ref, atol=1e-12)
+    # forgetting the exp(pm - M) weights must be visible
     bad1 = po.sum(-2) / pl.sum(-1)[..., None]
     assert not np.allclose(bad1, ref, atol=1e-6)
-    po2, pm2, pl2 = o.splitk_partials(q, k, v, 64)  # many empty splits
-    with np.errstate(over="ignore", invalid="ignore"):
-        big_m = pm2.max(-1, keepdims=True)
-        w = np.exp(pm2 - big_m)  # sentinel not skipped: -FLT_MAX - M underflows to 0 here,
-    bad2 = (w[..., None] * po2).sum(-2) / ((w * pl2).sum(-1)[..., None])
-    # ...so the skip is only observable through pm == -FLT_MAX being kept; make
-    # sure the combine really treats it as "no keys"
-    assert np.allclose(o.splitk_combine(po2, pm2, pl2, eps=0.0), ref, atol=1e-12)
-    assert np.allclose(bad2, ref, atol=1e-12)
+    # An empty split must carry the sentinel pm = -FLT_MAX: a partial writer
+    # that leaves (0, 0, 0) there instead moves the merge's reference max to
+    # 0.  With every real score far below 0 (all pm shifted by -1000, which
+    # leaves the exact result unchanged) the real splits' weights then
+    # underflow and the merge loses the output.
+    po2, pm2, pl2 = o.splitk_partials(q, k, v, 64)  # splits 40..63 are empty
+    empty = pm2 == -o.FLT_MAX
+    assert empty.any() and (~empty).any()
+    shifted = np.where(empty, pm2, pm2 - 1000.0)
+    assert np.allclose(o.splitk_combine(po2, shifted, pl2, eps=0.0), ref, atol=1e-12)
+    zero_sentinel = np.where(empty, 0.0, shifted)
+    with np.errstate(divide="ignore", invalid="ignore"):
+        bad2 = o.splitk_combine(po2, zero_sentinel, pl2, eps=0.0)
+    assert not np.allclose(bad2, ref, atol=1e-6)
