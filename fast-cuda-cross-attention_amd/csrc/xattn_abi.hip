@@ -8,6 +8,7 @@
 
 #include <algorithm>
 #include <mutex>
+#include <vector>
 
 #include "xattn_common.h"
 #include "xattn_launch.h"
@@ -76,103 +77,93 @@ int device_cu_count() {
 }
 
 // --------------------------------------------------------------------------
-// Library-owned split workspace of launch_optimized_kernel and
-// launch_wmma_kernel / launch_wmma_bf16_kernel: one grow-only buffer per
-// device, released with the process.  A split launch leases it from acquire
-// to release (the lock is held in between, so another host thread cannot
-// enqueue work on the buffer meanwhile).  Work on different streams never
-// uses the buffer at the same time: while every split launch has used one
-// stream, stream order alone serialises them and nothing is recorded (an
-// event after every launch measured 4.5 us per call at 64 latents x 784
-// keys); the first launch on another stream synchronises the device once,
-// and from then on an event is recorded after each launch's merge and the
-// next launch on a different stream waits for it.
+// Library-owned split workspaces of launch_optimized_kernel and
+// launch_wmma_kernel / launch_wmma_bf16_kernel: one block per (device,
+// stream), so split launches on different streams never share memory and
+// need no cross-stream ordering; on one stream, stream order serialises
+// them.  A block is allocated (hipMalloc) on a stream's first split launch
+// and replaced by a larger one, at least twice the size, when a launch needs
+// more.  A replaced block is never freed: launches already enqueued, or
+// kernels recorded into a graph, may still use it (its memory comes back at
+// process exit); geometric growth bounds the retired blocks' total by the
+// live block's size.  No launcher synchronises.  Under stream capture a
+// launch whose stream has a large enough block proceeds (the graph keeps
+// using that block, which is never freed); one that would have to allocate
+// is refused with XATTN_ERR_CAPTURE before anything is enqueued.
 // --------------------------------------------------------------------------
-struct Workspace {
-    void* ptr = nullptr;
-    size_t bytes = 0;
-    hipEvent_t done = nullptr;   // recorded after the last split launch's merge (multi)
-    hipStream_t last = nullptr;  // the stream of that launch
-    bool used = false;
-    bool multi = false;          // a second stream has used the buffer
+struct StreamWorkspace {
+    int dev;
+    hipStream_t stream;
+    void* ptr;
+    size_t bytes;
 };
 static std::mutex g_ws_mu;
-static Workspace g_ws[256];
+static std::vector<StreamWorkspace> g_ws;  // a handful of (device, stream) entries
+static std::vector<void*> g_ws_retired;     // replaced blocks, kept to process exit
+
+// Is `stream` recording a graph?  A query that fails counts as capturing
+// (the launcher then refuses rather than allocate blindly).
+static bool stream_capturing(hipStream_t stream) {
+    hipStreamCaptureStatus st = hipStreamCaptureStatusNone;
+    if (hipStreamIsCapturing(stream, &st) != hipSuccess) {
+        (void)hipGetLastError();
+        return true;
+    }
+    return st != hipStreamCaptureStatusNone;
+}
 
 class WorkspaceLease {
   public:
-    // The device's workspace of at least `bytes`, ordered after its previous
-    // user; nullptr (error recorded) on failure.
+    // The workspace of (current device, stream) with at least `bytes`;
+    // nullptr with an error recorded on failure.  The lock is held until
+    // release(), so no other host thread replaces the block between this
+    // launch's pointer lookup and its enqueue.
     void* acquire(size_t bytes, hipStream_t stream) {
         int dev = 0;
-        if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 256) {
+        if (hipGetDevice(&dev) != hipSuccess) {
+            (void)hipGetLastError();
             set_error(XATTN_ERR_ALLOC, "workspace: no current device");
             return nullptr;
         }
         lk_.lock();
-        dev_ = dev;
-        Workspace& w = g_ws[dev];
-        if (w.bytes < bytes) {
-            if (w.ptr) {
-                // Earlier launches may still read the old block.
-                (void)hipDeviceSynchronize();
-                (void)hipFree(w.ptr);
-                w.ptr = nullptr;
-                w.bytes = 0;
-                w.used = false;
-            }
-            void* p = nullptr;
-            if (hipMalloc(&p, bytes) != hipSuccess) {
-                (void)hipGetLastError();
-                set_error(XATTN_ERR_ALLOC, "workspace: hipMalloc(%zu) failed", bytes);
-                return nullptr;
-            }
-            w.ptr = p;
-            w.bytes = bytes;
+        StreamWorkspace* w = nullptr;
+        for (StreamWorkspace& e : g_ws)
+            if (e.dev == dev && e.stream == stream) w = &e;
+        if (w && w->bytes >= bytes) return w->ptr;
+        if (stream_capturing(stream)) {
+            set_error(XATTN_ERR_CAPTURE,
+                      "workspace: this split launch needs %zu bytes of workspace on a stream "
+                      "that is capturing a graph and has %zu; make one launch of this (or a "
+                      "larger) shape on the stream before capturing, or use "
+                      "launch_splitk_kernel with caller-owned scratch",
+                      bytes, w ? w->bytes : (size_t)0);
+            return nullptr;
         }
-        if (w.used && w.last != stream) {
-            if (!w.multi) {
-                // The first change of stream: no event covers the earlier
-                // launches, so wait for all of them.
-                if (!w.done &&
-                    hipEventCreateWithFlags(&w.done, hipEventDisableTiming) != hipSuccess) {
-                    (void)hipGetLastError();
-                    w.done = nullptr;
-                    set_error(XATTN_ERR_ALLOC, "workspace: hipEventCreateWithFlags failed");
-                    return nullptr;
-                }
-                if (hipDeviceSynchronize() != hipSuccess) {
-                    (void)hipGetLastError();
-                    set_error(XATTN_ERR_LAUNCH, "workspace: hipDeviceSynchronize failed");
-                    return nullptr;
-                }
-                w.multi = true;
-            } else if (hipStreamWaitEvent(stream, w.done, 0) != hipSuccess) {
-                (void)hipGetLastError();
-                set_error(XATTN_ERR_LAUNCH, "workspace: hipStreamWaitEvent failed");
-                return nullptr;
-            }
-        }
-        return w.ptr;
-    }
-    // The buffer is now in use by the work enqueued on `stream`.
-    void release(hipStream_t stream) {
-        if (dev_ < 0 || !lk_.owns_lock()) return;
-        Workspace& w = g_ws[dev_];
-        w.last = stream;
-        w.used = true;
-        if (w.multi && hipEventRecord(w.done, stream) != hipSuccess) {
+        size_t want = bytes;
+        if (w && want < 2 * w->bytes) want = 2 * w->bytes;
+        void* p = nullptr;
+        if (hipMalloc(&p, want) != hipSuccess) {
             (void)hipGetLastError();
-            // Without the event the next user must not overlap this one.
-            (void)hipStreamSynchronize(stream);
-            w.used = false;
+            set_error(XATTN_ERR_ALLOC, "workspace: hipMalloc(%zu) failed", want);
+            return nullptr;
         }
-        lk_.unlock();
+        if (w) {
+            g_ws_retired.push_back(w->ptr);
+            w->ptr = p;
+            w->bytes = want;
+        } else {
+            g_ws.push_back(StreamWorkspace{dev, stream, p, want});
+        }
+        return p;
     }
+    // The launch using the workspace has been enqueued.
+    void release() {
+        if (lk_.owns_lock()) lk_.unlock();
+    }
+    ~WorkspaceLease() { release(); }
 
   private:
     std::unique_lock<std::mutex> lk_{g_ws_mu, std::defer_lock};
-    int dev_ = -1;
 };
 
 // --------------------------------------------------------------------------
@@ -548,7 +539,7 @@ void launch_optimized_kernel(const float* Q, const float* K, const float* V, flo
     if (launch_flash_f32(ds, Q, K, V, nullptr, sc.po, sc.pm, sc.pl, batch_size, N_latent,
                          N_input, S, chunk, stream))
         launch_lse_combine(sc.po, sc.pm, sc.pl, output, batch_size * N_latent, S, stream);
-    lease.release(stream);
+    lease.release();
 }
 
 void launch_splitk_kernel(const float* Q, const float* K, const float* V, float* output,
@@ -596,7 +587,7 @@ static void wmma_common(bool bf16, const char* who, const uint16_t* Q, const uin
     if (launch_flash16(bf16, nw, Q, K, V, nullptr, sc.po, sc.pm, sc.pl, batch_size, N_latent,
                        N_input, S, chunk, stream))
         launch_lse_combine(sc.po, sc.pm, sc.pl, output, batch_size * N_latent, S, stream);
-    lease.release(stream);
+    lease.release();
 }
 
 static void wmma_splitk_common(bool bf16, const char* who, const uint16_t* Q, const uint16_t* K,

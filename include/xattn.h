@@ -12,12 +12,25 @@
  * (cuda_wrappers.py:83-175) bind unchanged; cudaStream_t becomes hipStream_t
  * (both opaque pointers; NULL is the null stream).
  *
- * Error behaviour: launchers return void, never synchronise and never
- * allocate caller-visible memory.  A launch the hardware rejects is reported
+ * Error behaviour: launchers return void and only enqueue work on `stream`;
+ * none calls hipDeviceSynchronize, hipStreamSynchronize, hipFree or any
+ * other synchronising function.  A launch the hardware rejects is reported
  * through hipGetLastError() as in the reference.  In addition, arguments a
  * kernel cannot run with (dim other than the kernel's supported dim, negative
  * sizes, num_splits < 1, NULL data pointers with non-zero sizes) are refused
  * before anything is launched and recorded for xattn_get_last_error().
+ *
+ * Allocation: every entry point works on caller-owned buffers, except that
+ * launch_optimized_kernel, launch_wmma_kernel and launch_wmma_bf16_kernel,
+ * when their plan splits the keys, keep the split partials in a
+ * library-owned workspace, one per (device, stream).  It is allocated with
+ * hipMalloc on the first such launch on a stream and replaced (hipMalloc of
+ * at least twice the size; the old block is kept, never freed, until the
+ * process exits) when a later launch on that stream needs more.  Launches
+ * on different streams never share a workspace.  While `stream` is capturing
+ * a graph, such a launch proceeds only if the stream's workspace is already
+ * large enough; otherwise it is refused with XATTN_ERR_CAPTURE and nothing
+ * is enqueued.  launch_splitk_kernel and its 16-bit twins never allocate.
  */
 #ifndef XATTN_H
 #define XATTN_H
@@ -56,8 +69,8 @@ void launch_tiled_kernel(const float* Q, const float* K, const float* V,
  * (v_mfma_f32_16x16x4_f32), online softmax in registers.  dim == 768.
  * Workgroups of 64, 32 or 16 latents and, where those cannot fill the device
  * cheaply, key splits merged by a log-sum-exp pass, as xattn_f32_plan
- * reports; split partials live in a library-owned device workspace that is
- * allocated on first need and grown (never shrunk) per device. */
+ * reports; split partials live in the stream's library-owned workspace (see
+ * "Allocation" above). */
 void launch_optimized_kernel(const float* Q, const float* K, const float* V,
                              float* output, int batch_size, int N_latent,
                              int N_input, int dim, hipStream_t stream);
@@ -81,7 +94,7 @@ void launch_splitk_kernel(const float* Q, const float* K, const float* V,
 /* Replaces launch_wmma_kernel, kernel_wmma.cu:139-154.  Q, K, V are IEEE
  * binary16 bit patterns; Q is pre-scaled by 1/sqrt(dim) by the caller
  * (cuda_wrappers.py:635-640).  dim == 768.  Launch shape and internal key
- * splits (library workspace, as above) as xattn_wmma_plan reports. */
+ * splits (stream's library workspace, as above) as xattn_wmma_plan reports. */
 void launch_wmma_kernel(const uint16_t* Q, const uint16_t* K,
                         const uint16_t* V, float* output, int batch_size,
                         int N_latent, int N_input, int dim,
@@ -116,7 +129,8 @@ enum {
     XATTN_ERR_INVALID_VALUE = 1, /* negative size, NULL pointer, bad splits */
     XATTN_ERR_UNSUPPORTED = 2,   /* shape the kernel is not built for      */
     XATTN_ERR_LAUNCH = 3,        /* the HIP runtime rejected the launch     */
-    XATTN_ERR_ALLOC = 4          /* workspace allocation failed             */
+    XATTN_ERR_ALLOC = 4,         /* workspace allocation failed             */
+    XATTN_ERR_CAPTURE = 5        /* would allocate while the stream captures */
 };
 
 /* Returns the first error recorded on this host thread since the last call,

@@ -1,9 +1,9 @@
-"""The library's internal split workspace under concurrent streams: shapes
-that launch_optimized_kernel and launch_wmma_bf16_kernel split over the keys
-(partials in the one per-device workspace) are launched alternately on two
-streams with different inputs.  Each split launch on the other stream waits
-for the previous one's merge, so both outputs must match the reference
-exactly as when run alone."""
+"""Split launches on two streams at once.  launch_optimized_kernel and
+launch_wmma_bf16_kernel keep split partials in a workspace per (device,
+stream); here a small and a larger split shape are launched alternately on
+two streams (and on the null stream), so each stream's workspace is grown
+while the other stream's launches are in flight.  Every output must match
+the float64 oracle as when run alone."""
 
 import ctypes
 
@@ -15,6 +15,7 @@ from conftest import fp32_gate
 pytestmark = pytest.mark.gpu
 
 P = ctypes.c_void_p
+SHAPES = [(1, 64, 784), (1, 256, 4096), (2, 48, 1500)]
 
 
 def _hip(cw):
@@ -28,49 +29,53 @@ def _hip(cw):
 
 @pytest.mark.parametrize("entry", ["launch_optimized_kernel", "launch_wmma_bf16_kernel"])
 def test_split_launches_on_two_streams(cw, oracle, entry):
-    b, nl, ni, d = 1, 64, 784, 768
     cu, _ = cw.device_info()
-    if entry == "launch_optimized_kernel":
-        assert cw.f32_plan(b, nl, ni, cu)[1] > 1  # the shape splits
-    else:
-        assert cw.wmma_plan(b, nl, ni, cu)[1] > 1
+    plan = cw.f32_plan if entry == "launch_optimized_kernel" else cw.wmma_plan
+    for b, nl, ni in SHAPES:
+        assert plan(b, nl, ni, cu)[1] > 1, (b, nl, ni)  # every shape splits
     hip = _hip(cw)
-    streams = [P(), P()]
-    for s in streams:
+    streams = [P(), P(), P(0)]
+    for s in streams[:2]:
         assert hip.hipStreamCreate(ctypes.byref(s)) == 0
-    bufs, outs, refs = [], [], []
+    cases = []  # (shape, args, out, ref) per (stream, shape)
     try:
-        for i in range(2):
-            q, k, v = oracle.make_inputs(b, nl, ni, d, seed=100 + i)
-            if entry == "launch_optimized_kernel":
-                ins = [cw.DeviceBuffer.holding(a) for a in (q, k, v)]
-                args = [p.f32 for p in ins]
-                refs.append(oracle.attention_f64(q, k, v))
-            else:
-                host = cw._half_inputs(q, k, v, b, d, bf16=True)
-                ins = [cw.DeviceBuffer.holding(a) for a in host]
-                args = [p.ptr for p in ins]
-                f = oracle.bf16_bits_to_f32
-                refs.append(oracle.attention_f64(
-                    f(host[0]).astype(np.float64) * np.sqrt(d), f(host[1]), f(host[2])))
-            out = cw.DeviceBuffer(b * nl * d * 4)
-            bufs += ins + [out]
-            outs.append((args, out))
+        for i in range(len(streams)):
+            row = []
+            for j, (b, nl, ni) in enumerate(SHAPES):
+                q, k, v = oracle.make_inputs(b, nl, ni, 768, seed=100 + 10 * i + j)
+                if entry == "launch_optimized_kernel":
+                    ins = [cw.DeviceBuffer.holding(a) for a in (q, k, v)]
+                    args = [p.f32 for p in ins]
+                    ref = oracle.attention_f64(q, k, v)
+                else:
+                    host = cw._half_inputs(q, k, v, b, 768, bf16=True)
+                    ins = [cw.DeviceBuffer.holding(a) for a in host]
+                    args = [p.ptr for p in ins]
+                    f = oracle.bf16_bits_to_f32
+                    ref = oracle.attention_f64(
+                        f(host[0]).astype(np.float64) * np.sqrt(768), f(host[1]), f(host[2]))
+                out = cw.DeviceBuffer(b * nl * 768 * 4).zero()
+                row.append(((b, nl, ni), ins, args, out, ref))
+            cases.append(row)
         fn = getattr(cw.lib, entry)
-        for _ in range(40):
-            for (args, out), s in zip(outs, streams):
-                fn(*args, out.f32, b, nl, ni, d, s)
+        for rep in range(12):
+            for i, s in enumerate(streams):
+                (b, nl, ni), _, args, out, _ = cases[i][(rep + i) % len(SHAPES)]
+                fn(*args, out.f32, b, nl, ni, 768, s)
         cw._lib_error_check(entry)
-        assert cw.cudart.cudaDeviceSynchronize() == 0
-        for (args, out), ref in zip(outs, refs):
-            got = out.download((b, nl, d))
-            if entry == "launch_optimized_kernel":
-                fp32_gate(got, ref)
-            else:
-                assert oracle.rel_err(got, ref) < 4e-3
+        assert cw.cudart.hipDeviceSynchronize() == 0
+        for row in cases:
+            for (b, nl, ni), _, _, out, ref in row:
+                got = out.download((b, nl, 768))
+                if entry == "launch_optimized_kernel":
+                    fp32_gate(got, ref)
+                else:
+                    assert oracle.rel_err(got, ref) < 4e-3, (b, nl, ni)
     finally:
-        assert cw.cudart.cudaDeviceSynchronize() == 0
-        for p in bufs:
-            p.close()
-        for s in streams:
+        assert cw.cudart.hipDeviceSynchronize() == 0
+        for row in cases:
+            for _, ins, _, out, _ in row:
+                for p in ins + [out]:
+                    p.close()
+        for s in streams[:2]:
             hip.hipStreamDestroy(s)
