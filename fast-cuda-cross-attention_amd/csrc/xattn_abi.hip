@@ -167,6 +167,48 @@ class WorkspaceLease {
 };
 
 // --------------------------------------------------------------------------
+// Static scratch of launch_optimized_kernel_noalloc: split partials live in a
+// file-scope device array instead of an allocated workspace.  Each GPU the
+// library runs on holds its own copy from module load until the process
+// ends.  On the host, `scratch` names a host-side stand-in, not device
+// memory: the device address is looked up once per device with
+// hipGetSymbolAddress (that device current) and only that address is handed
+// to kernels.  Every call on a GPU shares its copy; calls that overlap on
+// one GPU (different streams, or a graph replay beside an eager call) race.
+// Each launch overwrites every partial it merges (an empty split writes its
+// sentinel), so nothing has to be cleared between calls.
+// --------------------------------------------------------------------------
+constexpr size_t kNoallocScratchBytes = (size_t)64 << 20;  // 64 MiB per device
+static __device__ __align__(256) unsigned char scratch[kNoallocScratchBytes];
+
+static std::mutex g_scratch_mu;
+static void* g_scratch_ptr[256];
+
+// Device address of this device's `scratch`; nullptr (error recorded) if the
+// lookup fails.
+static void* noalloc_scratch(const char* who) {
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 256) {
+        (void)hipGetLastError();
+        set_error(XATTN_ERR_LAUNCH, "%s: no current device", who);
+        return nullptr;
+    }
+    std::lock_guard<std::mutex> lk(g_scratch_mu);
+    if (!g_scratch_ptr[dev]) {
+        void* ptr = nullptr;
+        const hipError_t e = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+        if (e != hipSuccess || !ptr) {
+            (void)hipGetLastError();
+            set_error(XATTN_ERR_LAUNCH, "%s: hipGetSymbolAddress(scratch) failed: %s", who,
+                      hipGetErrorString(e));
+            return nullptr;
+        }
+        g_scratch_ptr[dev] = ptr;
+    }
+    return g_scratch_ptr[dev];
+}
+
+// --------------------------------------------------------------------------
 // Validation
 // --------------------------------------------------------------------------
 bool validate_common(const char* who, const void* Q, const void* K, const void* V,
@@ -540,6 +582,46 @@ void launch_optimized_kernel(const float* Q, const float* K, const float* V, flo
                          N_input, S, chunk, stream))
         launch_lse_combine(sc.po, sc.pm, sc.pl, output, batch_size * N_latent, S, stream);
     lease.release();
+}
+
+void launch_optimized_kernel_noalloc(const float* Q, const float* K, const float* V,
+                                     float* output, int batch_size, int N_latent, int N_input,
+                                     int dim, hipStream_t stream) {
+    const char* who = "launch_optimized_kernel_noalloc";
+    if (!validate_common(who, Q, K, V, output, batch_size, N_latent, N_input, dim)) return;
+    if (!validate_dim768(who, dim)) return;
+    if (!validate_aligned16(who, Q, K, V, output, nullptr)) return;
+    if (batch_size == 0 || N_latent == 0) return;
+    // The plan of launch_optimized_kernel, so both give identical results.
+    int ds = 1, S = 1;
+    f32_plan(batch_size, N_latent, N_input, device_cu_count(), &ds, &S);
+    if (S <= 1) {
+        launch_flash_f32(ds, Q, K, V, output, nullptr, nullptr, nullptr, batch_size, N_latent,
+                         N_input, 1, N_input, stream);
+        return;
+    }
+    const size_t rows = (size_t)batch_size * N_latent;
+    const size_t po_bytes = rows * S * kDim * sizeof(float);
+    const size_t ml_bytes = rows * S * sizeof(float);
+    if (po_bytes + 2 * ml_bytes > kNoallocScratchBytes) {
+        set_error(XATTN_ERR_UNSUPPORTED,
+                  "%s: the plan for B=%d N_latent=%d N_input=%d takes %d key splits, whose "
+                  "partials need %zu bytes; the static scratch holds %zu (use "
+                  "launch_splitk_kernel with caller-owned scratch)",
+                  who, batch_size, N_latent, N_input, S, po_bytes + 2 * ml_bytes,
+                  kNoallocScratchBytes);
+        return;
+    }
+    char* base = (char*)noalloc_scratch(who);
+    if (!base) return;
+    float* po = (float*)base;
+    float* pm = (float*)(base + po_bytes);
+    float* pl = (float*)(base + po_bytes + ml_bytes);
+    const int tiles = (N_input + 15) / 16;
+    const int chunk = ((tiles + S - 1) / S) * 16;
+    if (launch_flash_f32(ds, Q, K, V, nullptr, po, pm, pl, batch_size, N_latent, N_input, S,
+                         chunk, stream))
+        launch_lse_combine(po, pm, pl, output, (int)rows, S, stream);
 }
 
 void launch_splitk_kernel(const float* Q, const float* K, const float* V, float* output,

@@ -221,6 +221,10 @@ HAS_SPLITK = _bind_optional("launch_splitk_kernel", _SPLITK_ARGS)
 HAS_WMMA_SPLITK = _bind_optional("launch_wmma_splitk_kernel", _WMMA_SPLITK_ARGS)
 HAS_WMMA_BF16 = _bind_optional("launch_wmma_bf16_kernel", _WMMA_ARGS)
 HAS_WMMA_SPLITK_BF16 = _bind_optional("launch_wmma_splitk_bf16_kernel", _WMMA_SPLITK_ARGS)
+# launch_optimized_kernel with its split partials in static device scratch:
+# for callers that cannot allocate (additive, no reference counterpart).
+HAS_NOALLOC = _bind_optional("launch_optimized_kernel_noalloc", [_F, _F, _F, _F, _I, _I, _I, _I,
+                                                                 _P])
 
 
 class DesignLimited(RuntimeError):

@@ -75,6 +75,20 @@ void launch_optimized_kernel(const float* Q, const float* K, const float* V,
                              float* output, int batch_size, int N_latent,
                              int N_input, int dim, hipStream_t stream);
 
+/* No counterpart in the reference: launch_optimized_kernel for callers that
+ * cannot allocate device memory (code under HIP graph capture, tight
+ * serving loops, harnesses that forbid hipMalloc).  Same plan, kernels and
+ * results, bit for bit; split partials go to a static scratch array of
+ * 64 MiB per device instead of the stream's workspace, and the call never
+ * allocates or frees.  A plan whose partials
+ * (batch_size * N_latent * splits * (dim + 2) * 4 bytes, splits from
+ * xattn_f32_plan) exceed 64 MiB is refused with XATTN_ERR_UNSUPPORTED.
+ * All calls on one GPU share its scratch: calls that overlap on a GPU (other
+ * streams, graph replays) race. */
+void launch_optimized_kernel_noalloc(const float* Q, const float* K, const float* V,
+                                     float* output, int batch_size, int N_latent,
+                                     int N_input, int dim, hipStream_t stream);
+
 /* ---- split-K (key-parallel) fp32 -------------------------------------- */
 
 /* Replaces launch_splitk_kernel, kernel_splitk.cu:238-251.

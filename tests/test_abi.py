@@ -201,6 +201,23 @@ def _call(cw, name, *args):
     return cw.lib.xattn_get_last_error(), cw.lib.xattn_get_last_error_string().decode()
 
 
+def test_noalloc_refuses_plans_past_its_scratch(cw):
+    """launch_optimized_kernel_noalloc takes launch_optimized_kernel's plan;
+    when that plan's split partials exceed the 64 MiB static scratch it is
+    refused before any HIP call (so no GPU is needed to see it)."""
+    F = ctypes.POINTER(ctypes.c_float)
+    dummy = ctypes.cast(ctypes.c_void_p(0x1000), F)
+    b, nl, ni = 28, 1792, 50176
+    lpw, s = cw.f32_plan(b, nl, ni, 256)
+    assert s > 1 and b * nl * s * 770 * 4 > (64 << 20)
+    code, msg = _call(cw, "launch_optimized_kernel_noalloc", dummy, dummy, dummy, dummy, b, nl,
+                      ni, 768, ctypes.c_void_p(0))
+    assert code == 2 and "static scratch" in msg and f"{s} key splits" in msg, msg
+    code, msg = _call(cw, "launch_optimized_kernel_noalloc", dummy, dummy, dummy, dummy, 1, 64,
+                      784, 100, ctypes.c_void_p(0))
+    assert code == 2 and "dim=100" in msg
+
+
 def test_validation_refuses_before_launch(cw):
     """Refused arguments never reach the HIP runtime (no GPU is needed)."""
     F = ctypes.POINTER(ctypes.c_float)
