@@ -101,6 +101,9 @@ def cpu_baseline(seconds):
 # (B, NL, NI, element type, entry point, Q std)
 CASES = {
     "cfg1": (1, 64, 784, "fp32", "launch_optimized_kernel", 1.0),
+    "cfg4-4096": (1, 256, 4096, "fp32", "launch_optimized_kernel", 0.02),
+    "cfg4-16384": (1, 256, 16384, "fp32", "launch_optimized_kernel", 0.02),
+    "cfg4-50176": (1, 256, 50176, "fp32", "launch_optimized_kernel", 0.02),
     "cfg4-splitk-4096": (1, 256, 4096, "fp32", "launch_splitk_kernel", 0.02),
     "cfg4-splitk-16384": (1, 256, 16384, "fp32", "launch_splitk_kernel", 0.02),
     "cfg4-splitk-50176": (1, 256, 50176, "fp32", "launch_splitk_kernel", 0.02),
