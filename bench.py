@@ -110,6 +110,7 @@ CASES = {
     "cfg5-fp16": (16, 512, 784, "fp16", "launch_wmma_kernel", 1.0),
     "cfg5-bf16": (16, 512, 784, "bf16", "launch_wmma_bf16_kernel", 1.0),
     "headline-bf16": (32, 1024, 784, "bf16", "launch_wmma_bf16_kernel", 1.0),
+    "headline-fp16": (32, 1024, 784, "fp16", "launch_wmma_kernel", 1.0),
 }
 
 
