@@ -210,6 +210,46 @@ def run_case(cw, name, steps, warmup):
     }
 
 
+def phase_clock(cw, name):
+    """Lifetime split of the 16-bit kernel's workgroups in the last launch of
+    case `name`, from a library built with `make phaseclock` (loaded through
+    XATTN_KERNELS_SO): per wavefront, cycles from start to the tile loop
+    (prologue: Q block, first tiles), in the loop, and after it (epilogue:
+    the O store); the shader clock from the 100 MHz real-time stamps; and
+    the workgroups' start times relative to the first (rounds show as
+    clusters)."""
+    fn = getattr(cw.lib, "xattn_phase_clock_read", None)
+    if fn is None:
+        raise RuntimeError("--phase-clock needs kernels_phaseclock.so (make phaseclock; "
+                           "XATTN_KERNELS_SO=<path> python bench.py ...)")
+    b, nl, ni, et, entry, _ = CASES[name]
+    if et == "fp32":
+        raise ValueError("--phase-clock instruments the 16-bit kernel only")
+    cu, _ = cw.device_info()
+    lpw, s = cw.wmma_plan(b, nl, ni, cu)
+    nw = lpw // 8
+    nblk = min(b * ((nl + lpw - 1) // lpw) * s, 4096)
+    raw = np.zeros((4096, 8, 6), dtype=np.uint64)
+    fn.argtypes = [ctypes.c_void_p, ctypes.c_size_t]
+    fn.restype = ctypes.c_int
+    if fn(raw.ctypes.data, raw.nbytes) != 0:
+        raise RuntimeError("xattn_phase_clock_read failed")
+    c = raw[:nblk, :nw].astype(np.int64)
+    pro, loop, epi = c[..., 1] - c[..., 0], c[..., 2] - c[..., 1], c[..., 3] - c[..., 2]
+    life = c[..., 3] - c[..., 0]
+    rt = c[..., 5] - c[..., 4]
+    start_us = (c[:, 0, 4] - c[:, 0, 4].min()) * 0.01
+    return {
+        "workgroups": int(nblk), "wavefronts": int(nw), "num_splits": int(s),
+        "clock_ghz": round(float(life.sum() / rt.sum() * 0.1), 3),
+        "cycles": {k: round(float(v.mean()), 0) for k, v in
+                   (("lifetime", life), ("prologue", pro), ("tile_loop", loop),
+                    ("epilogue", epi))},
+        "start_us_quantiles": [round(float(x), 2) for x in
+                               np.quantile(start_us, [0, 0.25, 0.5, 0.75, 1.0])],
+    }
+
+
 def copy_calibration(cw, mib, reps=5):
     """Plain device-to-device copy of `mib` MiB, `reps` times: reads and writes
     exactly mib MiB per copy, the reference point for FETCH_SIZE/WRITE_SIZE."""
@@ -234,6 +274,9 @@ def main():
     ap.add_argument("--case", choices=sorted(CASES), action="append",
                     help="run a secondary workload instead of the headline")
     ap.add_argument("--copy-calibration", type=int, metavar="MIB")
+    ap.add_argument("--phase-clock", action="store_true",
+                    help="with --case (16-bit) and a `make phaseclock` library: add the "
+                         "workgroups' prologue / tile loop / epilogue cycles")
     ap.add_argument("--launch-log", metavar="PATH",
                     help="also write every timed launch's event time (µs) to PATH as JSON")
     args = ap.parse_args()
@@ -249,7 +292,10 @@ def main():
         return
     if args.case:
         for name in args.case:
-            print(json.dumps(run_case(cw, name, args.steps, args.warmup)), flush=True)
+            rec = run_case(cw, name, args.steps, args.warmup)
+            if args.phase_clock:
+                rec["phase_clock"] = phase_clock(cw, name)
+            print(json.dumps(rec), flush=True)
         return
 
     cu, _ = cw.device_info()

@@ -144,6 +144,23 @@ __device__ inline lds_char* opaque_lds(unsigned byte_addr) {
     return (lds_char*)byte_addr;
 }
 
+#ifdef XATTN_PHASE_CLOCK
+// Instrumented builds only (`make phaseclock`; the product build compiles
+// none of this).  Per workgroup (the first kClockBlocks of a launch) and
+// wavefront: the shader clock at kernel start, tile-loop start, tile-loop
+// end and kernel end, then the 100 MHz real-time clock at start and end.
+// Each stamp sits where the wavefront has no LDS or scalar load in flight,
+// so its wait changes no overlap.
+constexpr int kClockBlocks = 4096;
+__device__ unsigned long long phase_clock[kClockBlocks][8][6];
+#define XATTN_STAMP(var)                                   \
+    __builtin_amdgcn_sched_barrier(0);                     \
+    const unsigned long long var = __builtin_amdgcn_s_memtime(); \
+    __builtin_amdgcn_sched_barrier(0)
+#else
+#define XATTN_STAMP(var) (void)0
+#endif
+
 template <typename T, bool PARTIAL, int NW>
 __global__ __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(NW / 4, NW / 4)))
 void flash16_kernel(Params p) {
@@ -156,6 +173,10 @@ void flash16_kernel(Params p) {
     __shared__ float sref[NCB * QB];   // the reference m_ref of each latent
     __shared__ int restart_flag;
 
+    XATTN_STAMP(clk_start);
+#ifdef XATTN_PHASE_CLOCK
+    const unsigned long long rt_start = __builtin_amdgcn_s_memrealtime();
+#endif
     const int item = xcd_remap(blockIdx.x, gridDim.x);
     const int rb = item % p.row_blocks;
     const int bs = item / p.row_blocks;
@@ -302,6 +323,7 @@ void flash16_kernel(Params p) {
     unsigned long long over;
     f4 acc[CBW][DB];  // O^T[d0 + 16t + 4g + i][q0 + 16(2h + cl) + j]
 
+    XATTN_STAMP(clk_loop);
     for (bool first = true;; first = false) {  // passes over the key range; a second is rare
         if (!first) issue(0);
         issue(1);
@@ -429,6 +451,7 @@ void flash16_kernel(Params p) {
         m_ref = fmaxf(hmax, stats[(w ^ 1) * QB + j].x);
         lds_barrier();
     }
+    XATTN_STAMP(clk_loop_end);
     wait_vmcnt<0>();  // the re-reads issued past the last phase
 
     // Combine the two key halves of each latent (max and sum, both against
@@ -485,11 +508,29 @@ void flash16_kernel(Params p) {
             else __builtin_nontemporal_store(o, at);
         }
     }
+#ifdef XATTN_PHASE_CLOCK
+    XATTN_STAMP(clk_end);
+    const unsigned long long rt_end = __builtin_amdgcn_s_memrealtime();
+    if (lane == 0 && blockIdx.x < (unsigned)kClockBlocks) {
+        unsigned long long* c = phase_clock[blockIdx.x][w];
+        c[0] = clk_start, c[1] = clk_loop, c[2] = clk_loop_end, c[3] = clk_end;
+        c[4] = rt_start, c[5] = rt_end;
+    }
+#endif
 }
 
 }  // namespace h16
 
 int h16_row_blocks(int NL, int nw) { return (NL + 8 * nw - 1) / (8 * nw); }
+
+#ifdef XATTN_PHASE_CLOCK
+// Copies the stamps of the last 16-bit launch: [block < 4096][wavefront <
+// 8][6] unsigned 64-bit values, as laid out above.  0 on success.
+extern "C" int xattn_phase_clock_read(void* dst, size_t bytes) {
+    const size_t n = bytes < sizeof(h16::phase_clock) ? bytes : sizeof(h16::phase_clock);
+    return hipMemcpyFromSymbol(dst, HIP_SYMBOL(h16::phase_clock), n) == hipSuccess ? 0 : 1;
+}
+#endif
 
 template <typename T, bool PARTIAL>
 static void launch16(int nw, dim3 grid, hipStream_t stream, const h16::Params& p) {
