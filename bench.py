@@ -111,6 +111,7 @@ CASES = {
     "cfg5-bf16": (16, 512, 784, "bf16", "launch_wmma_bf16_kernel", 1.0),
     "headline-bf16": (32, 1024, 784, "bf16", "launch_wmma_bf16_kernel", 1.0),
     "headline-fp16": (32, 1024, 784, "fp16", "launch_wmma_kernel", 1.0),
+    "headline-fp32": (32, 1024, 784, "fp32", "launch_optimized_kernel", 1.0),
 }
 
 
@@ -210,41 +211,60 @@ def run_case(cw, name, steps, warmup):
     }
 
 
-def phase_clock(cw, name):
-    """Lifetime split of the 16-bit kernel's workgroups in the last launch of
-    case `name`, from a library built with `make phaseclock` (loaded through
-    XATTN_KERNELS_SO): per wavefront, cycles from start to the tile loop
-    (prologue: Q block, first tiles), in the loop, and after it (epilogue:
-    the O store); the shader clock from the 100 MHz real-time stamps; and
-    the workgroups' start times relative to the first (rounds show as
-    clusters)."""
-    fn = getattr(cw.lib, "xattn_phase_clock_read", None)
-    if fn is None:
+def _phase_clock_fns(cw, et):
+    """(clear, read) of the phase-clock library for element type `et`."""
+    suffix = "f32" if et == "fp32" else "f16"
+    read = getattr(cw.lib, "xattn_phase_clock_read_" + suffix, None)
+    clear = getattr(cw.lib, "xattn_phase_clock_clear_" + suffix, None)
+    if read is None or clear is None:
         raise RuntimeError("--phase-clock needs kernels_phaseclock.so (make phaseclock; "
                            "XATTN_KERNELS_SO=<path> python bench.py ...)")
-    b, nl, ni, et, entry, _ = CASES[name]
-    if et == "fp32":
-        raise ValueError("--phase-clock instruments the 16-bit kernel only")
-    cu, _ = cw.device_info()
-    lpw, s = cw.wmma_plan(b, nl, ni, cu)
-    nw = lpw // 8
-    nblk = min(b * ((nl + lpw - 1) // lpw) * s, 4096)
-    raw = np.zeros((4096, 8, 6), dtype=np.uint64)
-    fn.argtypes = [ctypes.c_void_p, ctypes.c_size_t]
-    fn.restype = ctypes.c_int
-    if fn(raw.ctypes.data, raw.nbytes) != 0:
+    read.argtypes = [ctypes.c_void_p, ctypes.c_size_t]
+    read.restype = ctypes.c_int
+    clear.argtypes = []
+    clear.restype = ctypes.c_int
+    return clear, read
+
+
+def phase_clock_clear(cw, name):
+    clear, _ = _phase_clock_fns(cw, CASES[name][3])
+    if clear() != 0:
+        raise RuntimeError("xattn_phase_clock_clear failed")
+
+
+def phase_clock(cw, name):
+    """Lifetime split of the flash kernel's workgroups in the last launch of
+    case `name`, from a library built with `make phaseclock` (loaded through
+    XATTN_KERNELS_SO; cleared before the case runs): per wavefront, cycles
+    from start to the tile loop (prologue: Q block, first tiles), in the
+    loop, and after it (epilogue: the O store); for the fp32 kernel also the
+    loop's per-tile sums (waits at the tile barriers, the QK phase, the PV
+    phase); the shader clock from the 100 MHz real-time stamps; and the
+    workgroups' start times relative to the first (rounds show as
+    clusters).  Workgroups and wavefronts that left no stamps (past the
+    grid, or past the kernel's wavefronts) are not counted; a split launch's
+    merge kernel is not instrumented."""
+    _, read = _phase_clock_fns(cw, CASES[name][3])
+    raw = np.zeros((4096, 8, 9), dtype=np.uint64)
+    if read(raw.ctypes.data, raw.nbytes) != 0:
         raise RuntimeError("xattn_phase_clock_read failed")
+    live = raw[..., 3] != 0
+    nblk = int(live.any(axis=1).sum())
+    nw = int(live[0].sum())
+    if nblk == 0 or nw == 0:
+        raise RuntimeError(f"no phase-clock stamps after case {name}")
     c = raw[:nblk, :nw].astype(np.int64)
-    pro, loop, epi = c[..., 1] - c[..., 0], c[..., 2] - c[..., 1], c[..., 3] - c[..., 2]
     life = c[..., 3] - c[..., 0]
+    cycles = {"lifetime": life, "prologue": c[..., 1] - c[..., 0],
+              "tile_loop": c[..., 2] - c[..., 1], "epilogue": c[..., 3] - c[..., 2]}
+    if c[..., 6:9].any():
+        cycles.update({"loop_waits": c[..., 6], "loop_qk": c[..., 7], "loop_pv": c[..., 8]})
     rt = c[..., 5] - c[..., 4]
     start_us = (c[:, 0, 4] - c[:, 0, 4].min()) * 0.01
     return {
-        "workgroups": int(nblk), "wavefronts": int(nw), "num_splits": int(s),
+        "workgroups": nblk, "wavefronts": nw,
         "clock_ghz": round(float(life.sum() / rt.sum() * 0.1), 3),
-        "cycles": {k: round(float(v.mean()), 0) for k, v in
-                   (("lifetime", life), ("prologue", pro), ("tile_loop", loop),
-                    ("epilogue", epi))},
+        "cycles": {k: round(float(v.mean()), 0) for k, v in cycles.items()},
         "start_us_quantiles": [round(float(x), 2) for x in
                                np.quantile(start_us, [0, 0.25, 0.5, 0.75, 1.0])],
     }
@@ -275,8 +295,8 @@ def main():
                     help="run a secondary workload instead of the headline")
     ap.add_argument("--copy-calibration", type=int, metavar="MIB")
     ap.add_argument("--phase-clock", action="store_true",
-                    help="with --case (16-bit) and a `make phaseclock` library: add the "
-                         "workgroups' prologue / tile loop / epilogue cycles")
+                    help="with --case and a `make phaseclock` library: add the flash "
+                         "kernel's prologue / tile loop / epilogue cycles")
     ap.add_argument("--launch-log", metavar="PATH",
                     help="also write every timed launch's event time (µs) to PATH as JSON")
     args = ap.parse_args()
@@ -292,6 +312,8 @@ def main():
         return
     if args.case:
         for name in args.case:
+            if args.phase_clock:
+                phase_clock_clear(cw, name)
             rec = run_case(cw, name, args.steps, args.warmup)
             if args.phase_clock:
                 rec["phase_clock"] = phase_clock(cw, name)

@@ -151,6 +151,33 @@ __device__ inline void dma16_untracked(const void* sbase, unsigned voff, unsigne
         : "memory");
 }
 
+// --------------------------------------------------------------------------
+// Phase clock: instrumented builds only (`make phaseclock` defines
+// XATTN_PHASE_CLOCK; the product build compiles none of it).  A kernel
+// keeps, per workgroup (the first kClockBlocks of a launch) and wavefront,
+// kClockFields 64-bit values: the shader clock at kernel start, tile-loop
+// start, tile-loop end and kernel end; the 100 MHz real-time clock at start
+// and end; then, summed over the tiles (kernels that record them), the
+// cycles spent waiting for tiles at barriers, in the first phase of a tile
+// and in the second.  Each stamp sits where the wavefront has no LDS or
+// scalar load in flight, so its wait changes no overlap; the scheduling
+// barriers around it do pin the instruction order.
+// --------------------------------------------------------------------------
+constexpr int kClockBlocks = 4096;
+constexpr int kClockFields = 9;
+#ifdef XATTN_PHASE_CLOCK
+#define XATTN_STAMP(var)                                         \
+    __builtin_amdgcn_sched_barrier(0);                           \
+    const unsigned long long var = __builtin_amdgcn_s_memtime(); \
+    __builtin_amdgcn_sched_barrier(0)
+#define XATTN_CLOCK_DECL(...) unsigned long long __VA_ARGS__
+#define XATTN_CLOCK_ADD(acc, from, to) acc += (to) - (from)
+#else
+#define XATTN_STAMP(var) (void)0
+#define XATTN_CLOCK_DECL(...) (void)0
+#define XATTN_CLOCK_ADD(acc, from, to) (void)0
+#endif
+
 }  // namespace xattn
 
 // --------------------------------------------------------------------------

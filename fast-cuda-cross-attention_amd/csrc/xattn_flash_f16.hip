@@ -145,20 +145,8 @@ __device__ inline lds_char* opaque_lds(unsigned byte_addr) {
 }
 
 #ifdef XATTN_PHASE_CLOCK
-// Instrumented builds only (`make phaseclock`; the product build compiles
-// none of this).  Per workgroup (the first kClockBlocks of a launch) and
-// wavefront: the shader clock at kernel start, tile-loop start, tile-loop
-// end and kernel end, then the 100 MHz real-time clock at start and end.
-// Each stamp sits where the wavefront has no LDS or scalar load in flight,
-// so its wait changes no overlap.
-constexpr int kClockBlocks = 4096;
-__device__ unsigned long long phase_clock[kClockBlocks][8][6];
-#define XATTN_STAMP(var)                                   \
-    __builtin_amdgcn_sched_barrier(0);                     \
-    const unsigned long long var = __builtin_amdgcn_s_memtime(); \
-    __builtin_amdgcn_sched_barrier(0)
-#else
-#define XATTN_STAMP(var) (void)0
+// lifetime stamps of the last 16-bit launch (no per-tile sums)
+__device__ unsigned long long phase_clock[kClockBlocks][8][kClockFields];
 #endif
 
 template <typename T, bool PARTIAL, int NW>
@@ -514,7 +502,7 @@ void flash16_kernel(Params p) {
     if (lane == 0 && blockIdx.x < (unsigned)kClockBlocks) {
         unsigned long long* c = phase_clock[blockIdx.x][w];
         c[0] = clk_start, c[1] = clk_loop, c[2] = clk_loop_end, c[3] = clk_end;
-        c[4] = rt_start, c[5] = rt_end;
+        c[4] = rt_start, c[5] = rt_end, c[6] = c[7] = c[8] = 0;
     }
 #endif
 }
@@ -524,11 +512,17 @@ void flash16_kernel(Params p) {
 int h16_row_blocks(int NL, int nw) { return (NL + 8 * nw - 1) / (8 * nw); }
 
 #ifdef XATTN_PHASE_CLOCK
-// Copies the stamps of the last 16-bit launch: [block < 4096][wavefront <
-// 8][6] unsigned 64-bit values, as laid out above.  0 on success.
-extern "C" int xattn_phase_clock_read(void* dst, size_t bytes) {
+// The 16-bit kernel's stamps: [kClockBlocks][8 wavefronts][kClockFields]
+// unsigned 64-bit values.  Clear before a launch, read after.  0 on success.
+extern "C" int xattn_phase_clock_read_f16(void* dst, size_t bytes) {
     const size_t n = bytes < sizeof(h16::phase_clock) ? bytes : sizeof(h16::phase_clock);
     return hipMemcpyFromSymbol(dst, HIP_SYMBOL(h16::phase_clock), n) == hipSuccess ? 0 : 1;
+}
+extern "C" int xattn_phase_clock_clear_f16(void) {
+    void* ptr = nullptr;
+    if (hipGetSymbolAddress(&ptr, HIP_SYMBOL(h16::phase_clock)) != hipSuccess) return 1;
+    if (hipMemset(ptr, 0, sizeof(h16::phase_clock)) != hipSuccess) return 1;
+    return hipDeviceSynchronize() == hipSuccess ? 0 : 1;
 }
 #endif
 

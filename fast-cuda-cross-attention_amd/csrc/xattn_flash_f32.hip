@@ -85,6 +85,12 @@ __device__ inline f4 mfma4(float a, float b, f4 c) {
     return __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, c, 0, 0, 0);
 }
 
+#ifdef XATTN_PHASE_CLOCK
+// lifetime stamps and per-tile sums of the last fp32 launch: waits at the
+// two barriers, the QK phase (with the softmax when DS = 1), the PV phase
+__device__ unsigned long long phase_clock[kClockBlocks][8][kClockFields];
+#endif
+
 template <bool PARTIAL, int DS>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1)))
 void flash_f32_kernel(Params p) {
@@ -100,6 +106,10 @@ void flash_f32_kernel(Params p) {
     // tile buffers, the score exchange, then the restart flag (one LDS object)
     __shared__ __attribute__((aligned(16))) float lds[NBUF * BUF + XCH + 4];
 
+    XATTN_STAMP(clk_start);
+#ifdef XATTN_PHASE_CLOCK
+    const unsigned long long rt_start = __builtin_amdgcn_s_memrealtime();
+#endif
     const int item = xcd_remap(blockIdx.x, gridDim.x);
     const int rb = item % p.row_blocks;
     const int bs = item / p.row_blocks;
@@ -240,6 +250,8 @@ void flash_f32_kernel(Params p) {
         }
     };
 
+    XATTN_STAMP(clk_loop);
+    XATTN_CLOCK_DECL(pc_wait = 0, pc_qk = 0, pc_pv = 0);
     for (bool first = true;; first = false) {  // passes over the keys; a second is rare
         if (!first) {
             issue(0);
@@ -256,8 +268,10 @@ void flash_f32_kernel(Params p) {
             int ph = 2 * tile;
 
             // ---------------- QK phase ----------------
+            XATTN_STAMP(pc_a);
             wait_vmcnt<CPW>();      // this phase landed; phase ph+1 may be in flight
             lds_barrier();
+            XATTN_STAMP(pc_b);
             f4 s;
             {
                 // K operand reads run two 4-MFMA groups ahead; the sched_barrier
@@ -290,9 +304,11 @@ void flash_f32_kernel(Params p) {
             }
 
             // ---------------- PV phase ----------------
+            XATTN_STAMP(pc_c);
             ph += 1;
             wait_vmcnt<CPW>();
             lds_barrier();
+            XATTN_STAMP(pc_d);
             if constexpr (DS > 1) {
                 // Every wavefront of the block sums the shares in the same
                 // order, so all of them hold bit-identical scores and weights.
@@ -323,6 +339,11 @@ void flash_f32_kernel(Params p) {
                     __builtin_amdgcn_sched_barrier(0);
                 }
             }
+            XATTN_STAMP(pc_e);
+            XATTN_CLOCK_ADD(pc_wait, pc_a, pc_b);
+            XATTN_CLOCK_ADD(pc_wait, pc_c, pc_d);
+            XATTN_CLOCK_ADD(pc_qk, pc_b, pc_c);
+            XATTN_CLOCK_ADD(pc_pv, pc_d, pc_e);
         }
         // Every wavefront raises the flag (if at all) before this barrier, so
         // all of them read the same value.
@@ -339,6 +360,7 @@ void flash_f32_kernel(Params p) {
         lds_barrier();
     }
 
+    XATTN_STAMP(clk_loop_end);
     wait_vmcnt<0>();  // the re-reads issued past the last phase
 
     // The latent's exact max and sum of weights over its four lanes.
@@ -376,6 +398,15 @@ void flash_f32_kernel(Params p) {
         p.pm[pi] = m_true / sqrtf((float)kDim);
         p.pl[pi] = lsum * factor;
     }
+#ifdef XATTN_PHASE_CLOCK
+    XATTN_STAMP(clk_end);
+    const unsigned long long rt_end = __builtin_amdgcn_s_memrealtime();
+    if (lane == 0 && blockIdx.x < (unsigned)kClockBlocks) {
+        unsigned long long* c = phase_clock[blockIdx.x][w];
+        c[0] = clk_start, c[1] = clk_loop, c[2] = clk_loop_end, c[3] = clk_end;
+        c[4] = rt_start, c[5] = rt_end, c[6] = pc_wait, c[7] = pc_qk, c[8] = pc_pv;
+    }
+#endif
 }
 
 // Log-sum-exp merge of split partials (kernel_splitk.cu:186-236).  One
@@ -447,6 +478,22 @@ void lse_combine_kernel(const float* __restrict__ po, const float* __restrict__ 
 // --------------------------------------------------------------------------
 
 int f32_row_blocks(int NL, int ds) { return (NL + f32::BM / ds - 1) / (f32::BM / ds); }
+
+#ifdef XATTN_PHASE_CLOCK
+// The fp32 kernel's stamps: [kClockBlocks][8][kClockFields] unsigned 64-bit
+// values (four wavefronts used).  Clear before a launch, read after.  0 on
+// success.
+extern "C" int xattn_phase_clock_read_f32(void* dst, size_t bytes) {
+    const size_t n = bytes < sizeof(f32::phase_clock) ? bytes : sizeof(f32::phase_clock);
+    return hipMemcpyFromSymbol(dst, HIP_SYMBOL(f32::phase_clock), n) == hipSuccess ? 0 : 1;
+}
+extern "C" int xattn_phase_clock_clear_f32(void) {
+    void* ptr = nullptr;
+    if (hipGetSymbolAddress(&ptr, HIP_SYMBOL(f32::phase_clock)) != hipSuccess) return 1;
+    if (hipMemset(ptr, 0, sizeof(f32::phase_clock)) != hipSuccess) return 1;
+    return hipDeviceSynchronize() == hipSuccess ? 0 : 1;
+}
+#endif
 
 template <bool PARTIAL>
 static void launch_f32(int ds, unsigned nblk, hipStream_t stream, const f32::Params& p) {

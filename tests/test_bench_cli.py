@@ -28,74 +28,80 @@ def test_algorithmic_work_of_the_headline():
 
 
 class _FakeLib:
-    """Stands in for kernels_phaseclock.so: xattn_phase_clock_read fills the
-    [4096][8][6] stamp array with a chosen pattern."""
+    """Stands in for kernels_phaseclock.so: xattn_phase_clock_read_* fills
+    the [4096][8][9] stamp array with a chosen pattern."""
 
     def __init__(self, fill):
-        self.fill = fill
+        self.cleared = 0
 
         def read(dst, nbytes):
             import ctypes
 
             import numpy as np
             arr = np.ctypeslib.as_array((ctypes.c_uint64 * (nbytes // 8)).from_address(dst))
-            self.fill(arr.reshape(4096, 8, 6))
+            fill(arr.reshape(4096, 8, 9))
             return 0
 
-        self.xattn_phase_clock_read = read
+        def clear():
+            self.cleared += 1
+            return 0
+
+        self.xattn_phase_clock_read_f16 = self.xattn_phase_clock_read_f32 = read
+        self.xattn_phase_clock_clear_f16 = self.xattn_phase_clock_clear_f32 = clear
 
 
 class _FakeCw:
-    def __init__(self, fill, lpw, splits):
+    def __init__(self, fill):
         self.lib = _FakeLib(fill)
-        self.lpw, self.splits = lpw, splits
 
-    def device_info(self):
-        return 256, 160 * 1024
 
-    def wmma_plan(self, b, nl, ni, cu):
-        return self.lpw, self.splits
+def _fill_rounds(c, blocks, waves, tiles=False):
+    c[:] = 0
+    for b in range(blocks):
+        base = 1000 * b
+        c[b, :waves, 0] = base
+        c[b, :waves, 1] = base + 100      # prologue 100 cycles
+        c[b, :waves, 2] = base + 1100     # loop 1000
+        c[b, :waves, 3] = base + 1300     # epilogue 200; lifetime 1300
+        c[b, :waves, 4] = 5000 + (0 if b < blocks // 2 else 2600)  # two rounds, 26 us apart
+        c[b, :waves, 5] = c[b, :waves, 4] + 65  # 1300 cycles in 0.65 us: 2.0 GHz
+        if tiles:
+            c[b, :waves, 6], c[b, :waves, 7], c[b, :waves, 8] = 100, 450, 450
 
 
 def test_phase_clock_split_from_stamps():
     """phase_clock() turns the per-wavefront stamps (start, loop start, loop
     end, end; real-time start and end) into the prologue / loop / epilogue
-    means, the clock, and the workgroups' start-time quantiles; only the
-    launch's own workgroups and wavefronts count."""
+    means, the clock, and the workgroups' start-time quantiles; workgroups
+    and wavefronts that left no stamps do not count."""
     sys.path.insert(0, ROOT)
     import bench
 
-    def fill(c):
-        c[:] = 0
-        blocks = 32 * 16  # headline: B=32, NL=1024 in 64-latent workgroups
-        for b in range(blocks):
-            base = 1000 * b
-            c[b, :, 0] = base
-            c[b, :, 1] = base + 100      # prologue 100 cycles
-            c[b, :, 2] = base + 1100     # loop 1000
-            c[b, :, 3] = base + 1300     # epilogue 200; lifetime 1300
-            c[b, :, 4] = 5000 + (0 if b < 256 else 2600)  # two rounds, 26 us apart
-            c[b, :, 5] = c[b, :, 4] + 65  # 1300 cycles in 0.65 us: 2.0 GHz
-        c[blocks:, :, :] = 7  # stale stamps past the grid must not count
-
-    rec = bench.phase_clock(_FakeCw(fill, 64, 1), "headline-bf16")
+    cw = _FakeCw(lambda c: _fill_rounds(c, 512, 8))
+    bench.phase_clock_clear(cw, "headline-bf16")
+    assert cw.lib.cleared == 1
+    rec = bench.phase_clock(cw, "headline-bf16")
     assert rec["workgroups"] == 512 and rec["wavefronts"] == 8
     assert rec["cycles"] == {"lifetime": 1300.0, "prologue": 100.0, "tile_loop": 1000.0,
                              "epilogue": 200.0}
     assert rec["clock_ghz"] == 2.0
     assert rec["start_us_quantiles"][0] == 0.0 and rec["start_us_quantiles"][-1] == 26.0
 
+    # the fp32 kernel: four wavefronts, and the loop's per-tile sums
+    rec = bench.phase_clock(_FakeCw(lambda c: _fill_rounds(c, 512, 4, tiles=True)),
+                            "headline-fp32")
+    assert rec["wavefronts"] == 4
+    assert rec["cycles"]["loop_waits"] == 100.0 and rec["cycles"]["loop_qk"] == 450.0
 
-def test_phase_clock_refuses_fp32_and_product_library():
+
+def test_phase_clock_needs_the_instrumented_library():
     sys.path.insert(0, ROOT)
     import bench
     import pytest
-
-    cw = _FakeCw(lambda c: None, 64, 1)
-    with pytest.raises(ValueError):
-        bench.phase_clock(cw, "cfg1")
 
     class NoClock:
         lib = object()
     with pytest.raises(RuntimeError, match="phaseclock"):
         bench.phase_clock(NoClock(), "headline-bf16")
+    with pytest.raises(RuntimeError, match="no phase-clock stamps"):
+        bench.phase_clock(_FakeCw(lambda c: c.fill(0)), "cfg1")
