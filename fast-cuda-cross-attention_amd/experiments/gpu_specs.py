@@ -32,7 +32,6 @@ GPU_SPECS = {
         "peak_fp32_flops": 157.3 * TFLOP,
         "peak_fp16_tc_flops": 2516.6 * TFLOP,
         "peak_bf16_tc_flops": 2516.6 * TFLOP,
-        "peak_fp8_tc_flops": 5033.2 * TFLOP,
         "peak_bw_bytes": 8000.0 * GBs,
     },
     # AMD Instinct MI350X: the same gfx950 silicon at a 2.2 GHz peak clock.
@@ -44,7 +43,6 @@ GPU_SPECS = {
         "peak_fp32_flops": 144.2 * TFLOP,
         "peak_fp16_tc_flops": 2306.9 * TFLOP,
         "peak_bf16_tc_flops": 2306.9 * TFLOP,
-        "peak_fp8_tc_flops": 4613.7 * TFLOP,
         "peak_bw_bytes": 8000.0 * GBs,
     },
 }
@@ -53,9 +51,7 @@ GPU_SPECS = {
 PRECISION_PEAK_KEY = {
     "fp32": "peak_fp32_flops",
     "fp16": "peak_fp16_tc_flops",
-    "fp16_tc": "peak_fp16_tc_flops",
     "bf16": "peak_bf16_tc_flops",
-    "fp8": "peak_fp8_tc_flops",
 }
 
 

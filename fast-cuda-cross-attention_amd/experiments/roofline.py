@@ -19,7 +19,7 @@ this library's fp16/bf16 entry points write fp32 rows, so their callers pass
 out_precision="fp32".
 """
 
-BYTES_PER_ELEM = {"fp32": 4, "fp16": 2, "fp16_tc": 2, "bf16": 2, "fp8": 1}
+BYTES_PER_ELEM = {"fp32": 4, "fp16": 2, "bf16": 2}
 
 
 def flops(B, Nl, Ni, D):
