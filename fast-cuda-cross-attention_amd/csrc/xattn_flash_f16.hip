@@ -141,7 +141,7 @@ __device__ inline s4 tr_read(lds_s4* p) { return __builtin_amdgcn_ds_read_tr16_b
 // buffer offset to each, instead of one base register plus immediates.
 __device__ inline lds_char* opaque_lds(unsigned byte_addr) {
     asm volatile("" : "+v"(byte_addr));
-    return (lds_char*)byte_addr;
+    return (lds_char*)(uintptr_t)byte_addr;
 }
 
 #ifdef XATTN_PHASE_CLOCK
