@@ -272,20 +272,36 @@ void flash16_kernel(Params p) {
     };
 
     // Q^T operand of the score unit's block, k-step s:
-    // Q[q0 + 16 cbo + j][32s + 8g .. +7] (96 registers).  Latents past NL
-    // repeat the last one; they are not stored.  K(0) is requested first; the
-    // full wait after the Q loads leaves no compiler-visible load pending, so
-    // the compiler adds no waits inside the tile loop (where only untracked
-    // DMA is in flight).
+    // Q[q0 + 16 cbo + j][32s + 8g .. +7] (96 registers).  K(0) is requested
+    // first; no compiler-visible load is pending in the tile loop (where
+    // only untracked DMA is in flight).
     issue(0);
-    v8 qr[KSF];
     {
-        const int qc = min(qo, p.NL - 1);
-        const u16* qrow = p.Q + ((size_t)b * p.NL + qc) * kDim + 8 * g;
-#pragma unroll
-        for (int s = 0; s < KSF; ++s) qr[s] = *(const v8*)(qrow + 32 * s);
+        // The Q block arrives by the same DMA as the tiles, row-contiguous
+        // 1 KiB chunks into the buffers of phases 1 and 2 (free until the
+        // loop starts; 64 rows at the tile row stride fill both, 32 one),
+        // and every wavefront then reads its operand from LDS.  Latents past
+        // NL repeat the last one.
+        constexpr int QCH = BM * (LROW / 16) / kWave;  // 1 KiB chunks of the block
+        static_assert(QCH * 1024 == BM * LROW && BM * LROW <= 2 * BUFB, "Q staging");
+        const char* qsrc = uniform_ptr((const char*)(p.Q + ((size_t)b * p.NL + q0) * kDim));
+        const int qrows = p.NL - q0;  // >= 1
+        for (int m = w; m < QCH; m += NW) {
+            const int u = kWave * m + lane;
+            const int r = min(u / (LROW / 16), qrows - 1);
+            const int piece = min(u % (LROW / 16), ROWB / 16 - 1);
+            dma16_untracked(qsrc, (unsigned)(r * ROWB + 16 * piece), lds0 + BUFB + 1024u * m);
+        }
     }
     wait_vmcnt<0>();
+    lds_barrier();
+    v8 qr[KSF];
+    {
+        const lds_char* qrd = opaque_lds(lds0 + (unsigned)(BUFB + LROW * (QB * cbo + j) + 16 * g));
+#pragma unroll
+        for (int s = 0; s < KSF; ++s) qr[s] = *(const v8*)(qrd + 64 * s);
+    }
+    lds_barrier();  // the staging buffers take the tiles of phases 1 and 2 next
 
     // Per-lane LDS read bases within a tile buffer (fragments differ by
     // immediate offsets): K row 16 kbo + j at byte 16 g (k-step s adds 64 s);
