@@ -11,14 +11,16 @@
 //            S^T[16 keys x 16 q] = K[16k.., :] . Q[block c, :]^T       24 MFMA
 //            over all of D, then the unit's softmax and its half of the
 //            block's P^T operand, in the wavefront's own registers;
-//   output:  column slice a = w % 4 (192 columns) of latent blocks
-//            2h, 2h + 1, h = w / 4:
-//            O^T[slice x 32 q] += V[:, slice]^T . P^T[blocks]          12 x 2 MFMA
+//   output:  column slice w (96 columns) of all four latent blocks:
+//            O^T[slice x 64 q] += V[:, slice]^T . P^T[blocks]           6 x 4 MFMA
 //
 // so scores never cross wavefronts: the only exchange is the P operand (one
 // LDS write and read per block) plus, on the first tile and at restarts, the
-// weights' reference of a block's two owners.  Per tile, each SIMD issues 96
-// MFMAs; registers per lane: the Q block (96), the O^T accumulators (96).
+// weights' reference of a block's two owners.  Each V^T fragment feeds one
+// MFMA per latent block, so the CU reads each V tile from LDS once.  Per
+// tile, each SIMD issues 96 MFMAs; registers per lane: the Q block (96), the
+// O^T accumulators (96).  (NW = 4: two latent blocks, 192-column slices,
+// 12 x 2 MFMA.)
 //
 // Softmax by passes: a row's weights are exp2(s - m_ref) with m_ref fixed for
 // a pass (the row max of the first tile, shared by the two owners of the
@@ -59,12 +61,8 @@ namespace xattn {
 namespace h16 {
 
 constexpr int BN = 32;                 // keys per tile
-constexpr int NA = 4;                  // output column slices
 constexpr int QB = 16;                 // latents per MFMA block
-constexpr int CBW = 2;                 // latent blocks per wavefront in the output role
-constexpr int DW = kDim / NA;          // output columns per wavefront (192)
 constexpr int KSF = kDim / 32;         // k-steps of a full-D score chain (24)
-constexpr int DB = DW / 16;            // 16-column output blocks per wavefront (12)
 constexpr int ROWB = kDim * 2;         // bytes per K / V row in memory (1536)
 constexpr int LROW = ROWB + 32;        // bytes per tile row in LDS (1568)
 constexpr int BUFB = BN * LROW;        // bytes per tile buffer (49 KiB)
@@ -79,13 +77,15 @@ template <int NW>
 struct Shape {
     static constexpr int BM = 8 * NW;          // latents per workgroup
     static constexpr int NCB = BM / QB;        // latent blocks (4 or 2)
+    static constexpr int DW = kDim / NW;       // output columns per wavefront (96 or 192)
+    static constexpr int DB = DW / 16;         // 16-column output blocks per wavefront (6 or 12)
     static constexpr int CPW = CHUNKS / NW;    // DMA chunks per wavefront (6 or 12) ...
     // ... and wavefront 0 also issues the last one
     static constexpr int KPF = NW == 8 ? 3 : 4;  // K fragments read ahead of their MFMAs
-    static constexpr int VPF = NW == 8 ? 3 : 4;  // V column blocks read ahead of theirs
+    static constexpr int VPF = NW == 8 ? 2 : 4;  // V column blocks read ahead of theirs
     static constexpr int NCH = NW == 8 ? 2 : 4;  // score accumulator chains
-    static_assert(NCB * 2 == NW && (NW / NA) * CBW == NCB,
-                  "one score unit and one output slice per wavefront");
+    static_assert(NCB * 2 == NW && NCB * DB == 24,
+                  "one score unit and one output slice (all latents) per wavefront");
     static_assert(CHUNKS * 1024 == BUFB && CHUNKS == CPW * NW + 1, "DMA split");
     static_assert(NBUF * BUFB + NCB * kWave * 16 + NW * QB * 8 + NCB * QB * 4 + 4 <= 160 * 1024,
                   "LDS budget");
@@ -155,6 +155,7 @@ void flash16_kernel(Params p) {
     typedef typename Vec8<T>::type v8;
     typedef Shape<NW> Sh;
     constexpr int BM = Sh::BM, NCB = Sh::NCB, CPW = Sh::CPW, KPF = Sh::KPF, VPF = Sh::VPF;
+    constexpr int DW = Sh::DW, DB = Sh::DB;
     __shared__ __attribute__((aligned(16))) char lds[NBUF * BUFB];
     __shared__ __attribute__((aligned(16))) u4v pbuf[NCB * kWave];  // P^T operand per latent block
     __shared__ float2 stats[NW * QB];  // per owner and latent: (max, sum) or the reference
@@ -177,8 +178,7 @@ void flash16_kernel(Params p) {
     const int q0 = rb * BM;                     // first latent of the workgroup
     const int cbo = w >> 1, kbo = w & 1;        // score unit: latent block, key half
     const int qo = q0 + QB * cbo + j;           // ... and the latent of lane (j, *) in it
-    const int a = w % NA, h = w / NA;           // output role: column slice, latent half
-    const int d0 = a * DW;                      // first column of the slice
+    const int d0 = w * DW;                      // output role: first column of the slice
 
     int k0 = 0, k1 = p.NI;
     if (PARTIAL) {
@@ -195,8 +195,8 @@ void flash16_kernel(Params p) {
     if (k0 >= k1) {
         // empty key range: sentinel partials (kernel_wmma_splitk.cu:65-76) or zeros
 #pragma unroll
-        for (int cl = 0; cl < CBW; ++cl) {
-            const int q = q0 + QB * (CBW * h + cl) + j;
+        for (int cl = 0; cl < NCB; ++cl) {
+            const int q = q0 + QB * cl + j;
             if (q >= p.NL) continue;
             float* dst = out_row(q) + d0 + 4 * g;
 #pragma unroll
@@ -325,14 +325,14 @@ void flash16_kernel(Params p) {
     // the pass is checked once, at its end.  Its weights may then have
     // overflowed, but the whole pass is discarded and run again.
     unsigned long long over;
-    f4 acc[CBW][DB];  // O^T[d0 + 16t + 4g + i][q0 + 16(2h + cl) + j]
+    f4 acc[NCB][DB];  // O^T[d0 + 16t + 4g + i][q0 + 16cl + j]
 
     XATTN_STAMP(clk_loop);
     for (bool first = true;; first = false) {  // passes over the key range; a second is rare
         if (!first) issue(0);
         issue(1);
 #pragma unroll
-        for (int cl = 0; cl < CBW; ++cl)
+        for (int cl = 0; cl < NCB; ++cl)
 #pragma unroll
             for (int t = 0; t < DB; ++t) acc[cl][t] = (f4){0.f, 0.f, 0.f, 0.f};
         lsum = 0.f;
@@ -407,10 +407,10 @@ void flash16_kernel(Params p) {
             ph += 1;
             wait_vmcnt<CPW>();
             lds_barrier();
-            v8 pt[CBW];
+            v8 pt[NCB];
 #pragma unroll
-            for (int cl = 0; cl < CBW; ++cl)
-                pt[cl] = __builtin_bit_cast(v8, pbuf[(CBW * h + cl) * kWave + lane]);
+            for (int cl = 0; cl < NCB; ++cl)
+                pt[cl] = __builtin_bit_cast(v8, pbuf[cl * kWave + lane]);
             {
                 lds_s4* vr = (lds_s4*)opaque_lds(lds0 + (unsigned)((ph % NBUF) * BUFB + vread));  // 4 per 32 B
                 const Dma dv = dma_setup(ph + 2);
@@ -432,7 +432,7 @@ void flash16_kernel(Params p) {
                     const v8 vt = __builtin_bit_cast(
                         v8, __builtin_shufflevector(va[t], vc[t], 0, 1, 2, 3, 4, 5, 6, 7));
 #pragma unroll
-                    for (int cl = 0; cl < CBW; ++cl) acc[cl][t] = mfma32<T>(vt, pt[cl], acc[cl][t]);
+                    for (int cl = 0; cl < NCB; ++cl) acc[cl][t] = mfma32<T>(vt, pt[cl], acc[cl][t]);
                     __builtin_amdgcn_sched_barrier(0);
                 }
             }
@@ -468,16 +468,15 @@ void flash16_kernel(Params p) {
     if (g == 0) stats[w * QB + j] = make_float2(m_true, lsum);
     if (g == 0 && kbo == 0) sref[cbo * QB + j] = m_ref;
     lds_barrier();
-    float rsc[CBW];
+    float rsc[NCB];
 #pragma unroll
-    for (int cl = 0; cl < CBW; ++cl) {
-        const int cb = CBW * h + cl;
+    for (int cb = 0; cb < NCB; ++cb) {
         const float2 s0 = stats[(2 * cb) * QB + j], s1 = stats[(2 * cb + 1) * QB + j];
         const float mt = fmaxf(s0.x, s1.x);
         const float factor = fast_exp2((sref[cb * QB + j] - mt) * kLog2e);
         const float l = s0.y + s1.y;
-        rsc[cl] = PARTIAL ? factor : factor / (l * factor + 1e-6f);
-        if (PARTIAL && a == 0 && g == 0) {
+        rsc[cb] = PARTIAL ? factor : factor / (l * factor + 1e-6f);
+        if (PARTIAL && w == 0 && g == 0) {
             const int q = q0 + QB * cb + j;
             if (q < p.NL) {
                 const size_t pi = ((size_t)b * p.NL + q) * p.S + split;
@@ -488,18 +487,18 @@ void flash16_kernel(Params p) {
     }
     // The output leaves through the tile ring, free since the barrier above
     // (the DMA was drained after the loop): per latent block, each
-    // wavefront writes its 16 x 192 slice row-major into its own area, then
+    // wavefront writes its 16-row slice row-major into its own area, then
     // reads it back row-contiguous, so every store instruction covers whole
     // 128-byte lines of a row (the accumulator layout gives 64-byte halves).
     constexpr int SROW = DW * 4 + 16;  // padded staging row (bytes)
     static_assert(NW * QB * SROW <= NBUF * BUFB, "staging area");
     char* const stage = lds + w * (QB * SROW);
 #pragma unroll
-    for (int cl = 0; cl < CBW; ++cl) {
+    for (int cl = 0; cl < NCB; ++cl) {
 #pragma unroll
         for (int t = 0; t < DB; ++t)
             *(f4*)(stage + j * SROW + (16 * t + 4 * g) * 4) = acc[cl][t] * rsc[cl];
-        const int qb = q0 + QB * (CBW * h + cl);
+        const int qb = q0 + QB * cl;
 #pragma unroll
         for (int k = 0; k < QB * DW / 4 / kWave; ++k) {
             const int pc = k * kWave + lane;  // 16-byte piece of the slice
