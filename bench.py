@@ -164,8 +164,22 @@ def launch_stats(per_ms):
     }
 
 
-def run_case(cw, name, steps, warmup):
+def parse_plan(text):
+    """'LPW/CP/S' -> (latents per workgroup, column parts, key splits)."""
+    try:
+        lpw, cp, s = (int(x) for x in text.split("/"))
+    except ValueError:
+        raise argparse.ArgumentTypeError(f"plan {text!r} is not LPW/CP/S (e.g. 64/2/1)")
+    return lpw, cp, s
+
+
+def run_case(cw, name, steps, warmup, plan=None):
+    """Time case `name`; `plan` (16-bit cases only): run it through
+    launch_wmma_plan_kernel with that (latents per workgroup, column parts,
+    key splits) instead of the entry point's own plan."""
     b, nl, ni, et, entry, q_std = CASES[name]
+    if plan is not None and et == "fp32":
+        raise ValueError(f"--plan applies to the 16-bit cases, not {name}")
     cu, _ = cw.device_info()
     rng = np.random.RandomState(0)
     q = (rng.randn(b, nl, D) * q_std).astype(np.float32)
@@ -181,7 +195,12 @@ def run_case(cw, name, steps, warmup):
     stream = ctypes.c_void_p(0)
     fn = getattr(cw.lib, entry)
     note = {}
-    if entry == "launch_splitk_kernel":
+    if plan is not None:
+        fn = cw.lib.launch_wmma_plan_kernel
+        entry = "launch_wmma_plan_kernel"
+        note["plan"] = list(plan)
+        args = [int(et == "bf16")] + [p.ptr for p in bufs] + [out.f32, b, nl, ni, D, *plan, stream]
+    elif entry == "launch_splitk_kernel":
         s = cw.plan_num_splits(nl, ni, b, cu)
         extra = [cw.DeviceBuffer(b * nl * s * D * 4), cw.DeviceBuffer(b * nl * s * 4),
                  cw.DeviceBuffer(b * nl * s * 4)]
@@ -297,6 +316,9 @@ def main():
     ap.add_argument("--phase-clock", action="store_true",
                     help="with --case and a `make phaseclock` library: add the flash "
                          "kernel's prologue / tile loop / epilogue cycles")
+    ap.add_argument("--plan", type=parse_plan, metavar="LPW/CP/S",
+                    help="with --case (16-bit cases): launch through launch_wmma_plan_kernel "
+                         "with this plan (latents per workgroup / column parts / key splits)")
     ap.add_argument("--launch-log", metavar="PATH",
                     help="also write every timed launch's event time (µs) to PATH as JSON")
     args = ap.parse_args()
@@ -314,7 +336,7 @@ def main():
         for name in args.case:
             if args.phase_clock:
                 phase_clock_clear(cw, name)
-            rec = run_case(cw, name, args.steps, args.warmup)
+            rec = run_case(cw, name, args.steps, args.warmup, args.plan)
             if args.phase_clock:
                 rec["phase_clock"] = phase_clock(cw, name)
             print(json.dumps(rec), flush=True)

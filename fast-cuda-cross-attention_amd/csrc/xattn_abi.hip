@@ -353,62 +353,84 @@ int optimized_num_splits(int B, int NL, int NI, int cu) {
     return S;
 }
 
-// Modelled time (µs) of one 16-bit launch with nw wavefronts per workgroup
-// (8: 64 latents, 4: 32 latents) and S key splits of ct 32-key tiles each.
-// Fitted to launches on MI355X (256 CUs; 7 % mean error over B = 1..32,
-// N_latent = 64..1024, N_input = 784..50176): a 32-key tile costs a
-// workgroup 1.56 µs at 64 latents and 1.14 µs at 32, plus 5.45 µs per round
-// of workgroups (a round's Q loads and output stores reach HBM together); a
-// split launch adds the LSE merge, 1.86 µs + 0.31 µs per MB of partials
-// written and read back, + 0.06 µs per split while there are fewer merge rows
-// (B * N_latent) than CUs.
-static double h16_cost(int B, int NL, int cu, int nw, long long S, long long ct) {
-    const double tile_us = nw == 8 ? 1.559 : 1.140;
-    const long long W = (long long)B * h16_row_blocks(NL, nw) * S;
+// Launch forms of the 16-bit kernel: 64 latents on 8 wavefronts, 32 on 4,
+// and 64 latents on 8 wavefronts in two column halves (two workgroups per
+// row block, each computing the scores over all of D and half of the output).
+struct H16Form {
+    int nw, cp;
+};
+constexpr H16Form kH16Forms[] = {{8, 1}, {8, 2}, {4, 1}};
+
+// Modelled time (µs) of one 16-bit launch of form f with S key splits of ct
+// 32-key tiles each, fitted (least squares on relative error) to 582 timed
+// bf16 launches on MI355X: every form and split count the planner weighs at
+// 27 shapes, B = 1..32, N_latent = 64..1024, N_input = 784..50176
+// (experiments/wmma_plan_campaign.py, experiments/fit_wmma_cost.py).  Per
+// launch 3.22 µs; per round of workgroups, a 32-key tile costs 1.67 µs at 64
+// latents, 1.08 µs at 64 latents and half the columns, 1.22 µs at 32
+// latents, and 0.22 / 0.34 / 0.19 µs more when an unsplit launch fills every
+// CU (its workgroups then all stream K and V from L2 at once); the fit puts
+// no cost on a round beyond its tiles.  A split launch adds the LSE merge,
+// 8.75 µs + 0.39 µs per MB of partials written and read back + 0.08 µs per
+// split while there are fewer merge rows (B * N_latent) than CUs.  On those
+// shapes its choice is the fastest timed plan or within 4.4 % of it (0.44 %
+// mean), about the spread of repeated timings of one plan.
+static double h16_cost(int B, int NL, int cu, H16Form f, long long S, long long ct) {
+    const long long W = (long long)B * h16_row_blocks(NL, f.nw) * S * f.cp;
     const long long rounds = (W + cu - 1) / cu;
-    double t = (double)rounds * ((double)ct * tile_us + 5.449);
+    const bool full = S == 1 && W >= cu;
+    double tile_us = f.nw == 4 ? 1.224 : f.cp == 2 ? 1.078 : 1.671;
+    if (full) tile_us += f.nw == 4 ? 0.192 : f.cp == 2 ? 0.344 : 0.219;
+    double t = 3.218 + (double)rounds * (double)ct * tile_us;
     if (S > 1) {
         const double rows = (double)B * NL;
-        t += 1.862 + 0.308 * rows * (double)S * (kDim * 4) * 1e-6 +
-             0.061 * (double)S * std::max(0.0, 1.0 - rows / cu);
+        t += 8.754 + 0.389 * rows * (double)S * (kDim * 4) * 1e-6 +
+             0.078 * (double)S * std::max(0.0, 1.0 - rows / cu);
     }
     return t;
 }
 
-// Wavefronts per workgroup (8 or 4) for a 16-bit launch of S key splits of
-// `chunk` keys each: the cheaper by h16_cost.
-static int h16_shape_for(int B, int NL, int NI, int S, int chunk, int cu) {
+// Launch form of a 16-bit launch of S key splits of `chunk` keys each: the
+// cheapest by h16_cost.
+static H16Form h16_form_for(int B, int NL, int NI, int S, int chunk, int cu) {
     const long long ct = NI > 0 ? ((long long)std::min(chunk, NI) + 31) / 32 : 0;
-    return h16_cost(B, NL, cu, 4, S, ct) < h16_cost(B, NL, cu, 8, S, ct) ? 4 : 8;
+    H16Form best = kH16Forms[0];
+    double best_t = -1.0;
+    for (const H16Form& f : kH16Forms) {
+        const double t = h16_cost(B, NL, cu, f, S, ct);
+        if (best_t < 0.0 || t < best_t) best_t = t, best = f;
+    }
+    return best;
 }
 
-// Launch shape of the 16-bit entry points: the (wavefronts, S) pair of least
+// Launch plan of the 16-bit entry points: the (form, S) pair of least
 // h16_cost, S up to min(tiles, cu) whole 32-key tiles per split.  The last
-// shape is cached per thread.
-static void wmma_plan(int B, int NL, int NI, int cu, int* nw, int* S) {
-    thread_local int key[4] = {-1, -1, -1, -1}, val[2] = {8, 1};
+// plan is cached per thread.
+static void wmma_plan(int B, int NL, int NI, int cu, H16Form* form, int* S) {
+    thread_local int key[4] = {-1, -1, -1, -1}, val[3] = {8, 1, 1};
     if (key[0] == B && key[1] == NL && key[2] == NI && key[3] == cu) {
-        *nw = val[0];
-        *S = val[1];
+        *form = {val[0], val[1]};
+        *S = val[2];
         return;
     }
-    int bw = 8, bs = 1;
+    H16Form bf = kH16Forms[0];
+    int bs = 1;
     const long long tiles = NI > 0 ? ((long long)NI + 31) / 32 : 0;
     if (B > 0 && NL > 0 && tiles > 0) {
         double best_t = -1.0;
         const long long smax = std::min<long long>(tiles, cu);
-        for (int w = 8; w >= 4; w -= 4) {
+        for (const H16Form& f : kH16Forms) {
             for (long long s = 1; s <= smax; ++s) {
                 const long long ct = (tiles + s - 1) / s;
                 if ((tiles + ct - 1) / ct != s) continue;  // same chunks as a smaller s
-                const double t = h16_cost(B, NL, cu, w, s, ct);
-                if (best_t < 0.0 || t < best_t) best_t = t, bw = w, bs = (int)s;
+                const double t = h16_cost(B, NL, cu, f, s, ct);
+                if (best_t < 0.0 || t < best_t) best_t = t, bf = f, bs = (int)s;
             }
         }
     }
     key[0] = B, key[1] = NL, key[2] = NI, key[3] = cu;
-    val[0] = bw, val[1] = bs;
-    *nw = bw;
+    val[0] = bf.nw, val[1] = bf.cp, val[2] = bs;
+    *form = bf;
     *S = bs;
 }
 
@@ -503,15 +525,26 @@ int xattn_wmma_split_latents(int batch_size, int N_latent, int N_input, int num_
     if (batch_size < 1 || N_latent < 1 || num_splits < 1) return 64;
     long long chunk = ((long long)std::max(N_input, 0) + num_splits - 1) / num_splits;
     chunk = (chunk + 15) / 16 * 16;
-    return 8 * h16_shape_for(batch_size, N_latent, N_input, num_splits, (int)chunk,
-                             cu_count < 1 ? 1 : cu_count);
+    return 8 * h16_form_for(batch_size, N_latent, N_input, num_splits, (int)chunk,
+                            cu_count < 1 ? 1 : cu_count).nw;
 }
 
 void xattn_wmma_plan(int batch_size, int N_latent, int N_input, int cu_count,
                      int* latents_per_workgroup, int* num_splits) {
-    int nw = 8, S = 1;
-    wmma_plan(batch_size, N_latent, N_input, cu_count < 1 ? 1 : cu_count, &nw, &S);
-    if (latents_per_workgroup) *latents_per_workgroup = 8 * nw;
+    H16Form f;
+    int S = 1;
+    wmma_plan(batch_size, N_latent, N_input, cu_count < 1 ? 1 : cu_count, &f, &S);
+    if (latents_per_workgroup) *latents_per_workgroup = 8 * f.nw;
+    if (num_splits) *num_splits = S;
+}
+
+void xattn_wmma_plan_ex(int batch_size, int N_latent, int N_input, int cu_count,
+                        int* latents_per_workgroup, int* column_parts, int* num_splits) {
+    H16Form f;
+    int S = 1;
+    wmma_plan(batch_size, N_latent, N_input, cu_count < 1 ? 1 : cu_count, &f, &S);
+    if (latents_per_workgroup) *latents_per_workgroup = 8 * f.nw;
+    if (column_parts) *column_parts = f.cp;
     if (num_splits) *num_splits = S;
 }
 
@@ -647,17 +680,13 @@ void launch_splitk_kernel(const float* Q, const float* K, const float* V, float*
     launch_lse_combine(po, pm, pl, output, batch_size * N_latent, num_splits, stream);
 }
 
-static void wmma_common(bool bf16, const char* who, const uint16_t* Q, const uint16_t* K,
-                        const uint16_t* V, float* output, int batch_size, int N_latent,
-                        int N_input, int dim, hipStream_t stream) {
-    if (!validate_common(who, Q, K, V, output, batch_size, N_latent, N_input, dim)) return;
-    if (!validate_dim768(who, dim)) return;
-    if (!validate_aligned16(who, Q, K, V, output, nullptr)) return;
-    if (batch_size == 0 || N_latent == 0) return;
-    int nw = 8, S = 1;
-    wmma_plan(batch_size, N_latent, N_input, device_cu_count(), &nw, &S);
+// A 16-bit launch with a given plan: form f, S key splits of whole 32-key
+// tiles (partials in the stream's library workspace when S > 1).
+static void wmma_run(bool bf16, const uint16_t* Q, const uint16_t* K, const uint16_t* V,
+                     float* output, int batch_size, int N_latent, int N_input, H16Form f, int S,
+                     hipStream_t stream) {
     if (S <= 1) {
-        launch_flash16(bf16, nw, Q, K, V, output, nullptr, nullptr, nullptr, batch_size,
+        launch_flash16(bf16, f.nw, f.cp, Q, K, V, output, nullptr, nullptr, nullptr, batch_size,
                        N_latent, N_input, 1, N_input, stream);
         return;
     }
@@ -666,10 +695,23 @@ static void wmma_common(bool bf16, const char* who, const uint16_t* Q, const uin
     SplitScratch sc;
     WorkspaceLease lease;
     if (!split_scratch(&sc, lease, batch_size, N_latent, S, stream)) return;
-    if (launch_flash16(bf16, nw, Q, K, V, nullptr, sc.po, sc.pm, sc.pl, batch_size, N_latent,
-                       N_input, S, chunk, stream))
+    if (launch_flash16(bf16, f.nw, f.cp, Q, K, V, nullptr, sc.po, sc.pm, sc.pl, batch_size,
+                       N_latent, N_input, S, chunk, stream))
         launch_lse_combine(sc.po, sc.pm, sc.pl, output, batch_size * N_latent, S, stream);
     lease.release();
+}
+
+static void wmma_common(bool bf16, const char* who, const uint16_t* Q, const uint16_t* K,
+                        const uint16_t* V, float* output, int batch_size, int N_latent,
+                        int N_input, int dim, hipStream_t stream) {
+    if (!validate_common(who, Q, K, V, output, batch_size, N_latent, N_input, dim)) return;
+    if (!validate_dim768(who, dim)) return;
+    if (!validate_aligned16(who, Q, K, V, output, nullptr)) return;
+    if (batch_size == 0 || N_latent == 0) return;
+    H16Form f;
+    int S = 1;
+    wmma_plan(batch_size, N_latent, N_input, device_cu_count(), &f, &S);
+    wmma_run(bf16, Q, K, V, output, batch_size, N_latent, N_input, f, S, stream);
 }
 
 static void wmma_splitk_common(bool bf16, const char* who, const uint16_t* Q, const uint16_t* K,
@@ -688,10 +730,10 @@ static void wmma_splitk_common(bool bf16, const char* who, const uint16_t* Q, co
     // kernel_wmma_splitk.cu:52: chunk = ceil(NI / S) rounded up to a multiple of 16
     long long chunk = ((long long)N_input + num_splits - 1) / num_splits;
     chunk = (chunk + 15) / 16 * 16;
-    const int nw = h16_shape_for(batch_size, N_latent, N_input, num_splits, (int)chunk,
-                                 device_cu_count());
-    if (!launch_flash16(bf16, nw, Q, K, V, nullptr, po, pm, pl, batch_size, N_latent, N_input,
-                        num_splits, (int)chunk, stream))
+    const H16Form f = h16_form_for(batch_size, N_latent, N_input, num_splits, (int)chunk,
+                                   device_cu_count());
+    if (!launch_flash16(bf16, f.nw, f.cp, Q, K, V, nullptr, po, pm, pl, batch_size, N_latent,
+                        N_input, num_splits, (int)chunk, stream))
         return;
     launch_lse_combine(po, pm, pl, output, batch_size * N_latent, num_splits, stream);
 }
@@ -708,6 +750,33 @@ void launch_wmma_bf16_kernel(const uint16_t* Q, const uint16_t* K, const uint16_
                              hipStream_t stream) {
     wmma_common(true, "launch_wmma_bf16_kernel", Q, K, V, output, batch_size, N_latent,
                 N_input, dim, stream);
+}
+
+void launch_wmma_plan_kernel(int bf16, const uint16_t* Q, const uint16_t* K, const uint16_t* V,
+                             float* output, int batch_size, int N_latent, int N_input, int dim,
+                             int latents_per_workgroup, int column_parts, int num_splits,
+                             hipStream_t stream) {
+    const char* who = "launch_wmma_plan_kernel";
+    if (!validate_common(who, Q, K, V, output, batch_size, N_latent, N_input, dim)) return;
+    if (!validate_dim768(who, dim)) return;
+    if (!validate_aligned16(who, Q, K, V, output, nullptr)) return;
+    const bool form_ok = (latents_per_workgroup == 64 && (column_parts == 1 || column_parts == 2)) ||
+                         (latents_per_workgroup == 32 && column_parts == 1);
+    if (!form_ok) {
+        set_error(XATTN_ERR_INVALID_VALUE, "%s: no form of %d latents per workgroup in %d column "
+                  "parts (64 in 1 or 2, 32 in 1)", who, latents_per_workgroup, column_parts);
+        return;
+    }
+    const int tiles = (N_input + 31) / 32;
+    if (num_splits < 1 || num_splits > std::max(tiles, 1)) {
+        set_error(XATTN_ERR_INVALID_VALUE, "%s: num_splits %d outside 1..%d (32-key tiles)", who,
+                  num_splits, std::max(tiles, 1));
+        return;
+    }
+    if (batch_size == 0 || N_latent == 0) return;
+    wmma_run(bf16 != 0, Q, K, V, output, batch_size, N_latent, N_input,
+             H16Form{latents_per_workgroup / 8, column_parts}, N_input == 0 ? 1 : num_splits,
+             stream);
 }
 
 void launch_wmma_splitk_kernel(const uint16_t* Q, const uint16_t* K, const uint16_t* V,

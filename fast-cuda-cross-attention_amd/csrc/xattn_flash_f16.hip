@@ -72,21 +72,31 @@ constexpr int CHUNKS = BUFB / 1024;    // 1 KiB DMA chunks per tile (49)
 // Workgroup shapes.  NW = 8: two wavefronts per SIMD, 64 latents; NW = 4: one
 // per SIMD, 32 latents (twice the workgroups for a given NL, for shapes whose
 // 64-latent blocks cannot fill the device: no key split, no merge pass).
+// CP = 2 (NW = 8 only): the workgroup computes the scores of its 64 latents
+// over all of D but only half of the output columns, and its twin the other
+// half: twice the workgroups again, each streaming all of K but half of V
+// (74 instead of 98 KiB per tile), for 1.5x the MFMA work per output.
 // Either way each wavefront owns one score unit and one output slice.
-template <int NW>
+template <int NW, int CP>
 struct Shape {
     static constexpr int BM = 8 * NW;          // latents per workgroup
     static constexpr int NCB = BM / QB;        // latent blocks (4 or 2)
-    static constexpr int DW = kDim / NW;       // output columns per wavefront (96 or 192)
-    static constexpr int DB = DW / 16;         // 16-column output blocks per wavefront (6 or 12)
-    static constexpr int CPW = CHUNKS / NW;    // DMA chunks per wavefront (6 or 12) ...
-    // ... and wavefront 0 also issues the last one
+    static constexpr int DWC = kDim / CP;      // output columns per workgroup (768 or 384)
+    static constexpr int DW = DWC / NW;        // output columns per wavefront (96, 192 or 48)
+    static constexpr int DB = DW / 16;         // 16-column output blocks per wavefront
+    static constexpr int LROWV = DWC * 2 + 32;  // bytes per V tile row in LDS (1568 or 800)
+    static constexpr int CHUNKSV = BN * LROWV / 1024;  // DMA chunks per V tile (49 or 25)
+    static constexpr int CPW = CHUNKS / NW;    // DMA chunks per wavefront per K tile (6 or 12) ...
+    static constexpr int CPWV = CHUNKSV / NW;  // ... and per V tile (6, 12 or 3); wavefront
+    // 0 also issues the last chunk of each
     static constexpr int KPF = NW == 8 ? 3 : 4;  // K fragments read ahead of their MFMAs
     static constexpr int VPF = NW == 8 ? 2 : 4;  // V column blocks read ahead of theirs
     static constexpr int NCH = NW == 8 ? 2 : 4;  // score accumulator chains
-    static_assert(NCB * 2 == NW && NCB * DB == 24,
+    static_assert(NCB * 2 == NW && NCB * DB * CP == 24 && (CP == 1 || NW == 8),
                   "one score unit and one output slice (all latents) per wavefront");
     static_assert(CHUNKS * 1024 == BUFB && CHUNKS == CPW * NW + 1, "DMA split");
+    static_assert(CHUNKSV * 1024 == BN * LROWV && CHUNKSV == CPWV * NW + 1 && DB % CPWV == 0,
+                  "V DMA split");
     static_assert(NBUF * BUFB + NCB * kWave * 16 + NW * QB * 8 + NCB * QB * 4 + 4 <= 160 * 1024,
                   "LDS budget");
 };
@@ -145,17 +155,20 @@ __device__ inline lds_char* opaque_lds(unsigned byte_addr) {
 }
 
 #ifdef XATTN_PHASE_CLOCK
-// lifetime stamps of the last 16-bit launch (no per-tile sums)
+// lifetime stamps and per-tile sums of the last 16-bit launch: waits at the
+// two barriers, the score phase (with the softmax and the P write), the
+// output phase
 __device__ unsigned long long phase_clock[kClockBlocks][8][kClockFields];
 #endif
 
-template <typename T, bool PARTIAL, int NW>
+template <typename T, bool PARTIAL, int NW, int CP>
 __global__ __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(NW / 4, NW / 4)))
 void flash16_kernel(Params p) {
     typedef typename Vec8<T>::type v8;
-    typedef Shape<NW> Sh;
+    typedef Shape<NW, CP> Sh;
     constexpr int BM = Sh::BM, NCB = Sh::NCB, CPW = Sh::CPW, KPF = Sh::KPF, VPF = Sh::VPF;
-    constexpr int DW = Sh::DW, DB = Sh::DB;
+    constexpr int DW = Sh::DW, DB = Sh::DB, DWC = Sh::DWC, LROWV = Sh::LROWV;
+    constexpr int CPWV = Sh::CPWV, CHUNKSV = Sh::CHUNKSV;
     __shared__ __attribute__((aligned(16))) char lds[NBUF * BUFB];
     __shared__ __attribute__((aligned(16))) u4v pbuf[NCB * kWave];  // P^T operand per latent block
     __shared__ float2 stats[NW * QB];  // per owner and latent: (max, sum) or the reference
@@ -166,9 +179,12 @@ void flash16_kernel(Params p) {
 #ifdef XATTN_PHASE_CLOCK
     const unsigned long long rt_start = __builtin_amdgcn_s_memrealtime();
 #endif
+    // The CP column parts of a row block are consecutive items, so they run
+    // on one XCD and share its K tiles and Q block in L2.
     const int item = xcd_remap(blockIdx.x, gridDim.x);
-    const int rb = item % p.row_blocks;
-    const int bs = item / p.row_blocks;
+    const int ch = CP == 1 ? 0 : item % CP;  // output column part
+    const int rb = (item / CP) % p.row_blocks;
+    const int bs = item / CP / p.row_blocks;
     const int split = bs % p.S;
     const int b = bs / p.S;
 
@@ -178,7 +194,7 @@ void flash16_kernel(Params p) {
     const int q0 = rb * BM;                     // first latent of the workgroup
     const int cbo = w >> 1, kbo = w & 1;        // score unit: latent block, key half
     const int qo = q0 + QB * cbo + j;           // ... and the latent of lane (j, *) in it
-    const int d0 = w * DW;                      // output role: first column of the slice
+    const int d0 = ch * DWC + w * DW;           // output role: first column of the slice
 
     int k0 = 0, k1 = p.NI;
     if (PARTIAL) {
@@ -202,7 +218,7 @@ void flash16_kernel(Params p) {
 #pragma unroll
             for (int e = 0; e < DB; ++e) *(f4*)(dst + 16 * e) = (f4){0.f, 0.f, 0.f, 0.f};
         }
-        if (PARTIAL && kbo == 0 && g == 0 && qo < p.NL) {
+        if (PARTIAL && ch == 0 && kbo == 0 && g == 0 && qo < p.NL) {
             const size_t pi = ((size_t)b * p.NL + qo) * p.S + split;
             p.pm[pi] = -FLT_MAX;
             p.pl[pi] = 0.f;
@@ -210,9 +226,10 @@ void flash16_kernel(Params p) {
         return;
     }
 
-    // K and V rows of this split's key range; keys are counted from k0 below.
+    // K rows and this column part's V columns of the split's key range; keys
+    // are counted from k0 below.
     const char* Kb = (const char*)(p.K + ((size_t)b * p.NI + k0) * kDim);
-    const char* Vb = (const char*)(p.V + ((size_t)b * p.NI + k0) * kDim);
+    const char* Vb = (const char*)(p.V + ((size_t)b * p.NI + k0) * kDim + ch * DWC);
     const int nk = k1 - k0;
     // Non-empty (the early return above); without these facts the compiler
     // guards the tile loop for zero trips and the split-K instantiation no
@@ -229,21 +246,31 @@ void flash16_kernel(Params p) {
     // rows past the range re-read its last row instead (clamped below).
     auto row_lo = [&](int tile) { return (tile == ntiles - 1 && nk >= BN) ? BN - (nk - tile * BN) : 0; };
 
-    // DMA.  Chunk m of a tile covers LDS bytes [1024 m, 1024 m + 1024): lane i
-    // lands on 16-byte slot u = 64 m + i, row u / 98, piece u % 98 (pieces 96
-    // and 97 are padding, which re-read piece 95).  Wavefront w issues chunks
-    // CPW w .. CPW w + CPW - 1, and wavefront 0 also chunk 48.  The per-lane source
-    // offsets are the same for every tile; the DMA is untracked
-    // (dma16_untracked): the phase waits order it.  Phases past the end re-read
-    // the last phase of the same kind into the buffer of phase ph - 3, whose
-    // readers are done, so every tile issues the same way; the DMA is drained
-    // after the loop.
+    // DMA.  Chunk m of a K tile covers LDS bytes [1024 m, 1024 m + 1024): lane
+    // i lands on 16-byte slot u = 64 m + i, row u / 98, piece u % 98 (pieces
+    // 96 and 97 are padding, which re-read piece 95).  Wavefront w issues
+    // chunks CPW w .. CPW w + CPW - 1, and wavefront 0 also chunk 48.  A V
+    // tile is laid out the same way at its own row stride (LROWV: 50 pieces
+    // and 25 chunks when the workgroup holds half of the columns).  The
+    // per-lane source offsets are the same for every tile; the DMA is
+    // untracked (dma16_untracked): the phase waits order it.  Phases past the
+    // end re-read the last phase of the same kind into the buffer of phase
+    // ph - 3, whose readers are done, so every tile issues the same way; the
+    // DMA is drained after the loop.
+    auto chunk_offset = [&](int m, int row_pieces, int data_pieces) {
+        const int u = 64 * m + lane;
+        const int r = u / row_pieces, piece = min(u - r * row_pieces, data_pieces - 1);
+        return (unsigned)(min(r, nk - 1) * ROWB + 16 * piece);
+    };
     unsigned doff[CPW + 1];
 #pragma unroll
-    for (int t = 0; t <= CPW; ++t) {
-        const int u = 64 * (t < CPW ? CPW * w + t : CHUNKS - 1) + lane;  // t = CPW: chunk 48
-        const int r = u / (LROW / 16), piece = min(u - r * (LROW / 16), ROWB / 16 - 1);
-        doff[t] = (unsigned)(min(r, nk - 1) * ROWB + 16 * piece);
+    for (int t = 0; t <= CPW; ++t)  // t = CPW: chunk 48
+        doff[t] = chunk_offset(t < CPW ? CPW * w + t : CHUNKS - 1, LROW / 16, ROWB / 16);
+    unsigned doffv[CP == 1 ? 1 : CPWV + 1];
+    if constexpr (CP > 1) {
+#pragma unroll
+        for (int t = 0; t <= CPWV; ++t)
+            doffv[t] = chunk_offset(t < CPWV ? CPWV * w + t : CHUNKSV - 1, LROWV / 16, DWC / 8);
     }
     const unsigned lds0 = lds_u32(lds);
     struct Dma {
@@ -258,17 +285,32 @@ void flash16_kernel(Params p) {
         d.m0 = lds0 + (unsigned)((ph % NBUF) * BUFB);
         return d;
     };
-    auto dma_chunk = [&](const Dma& d, int t) {
+    // chunk t (< CPW) of a K phase / (< CPWV) of a V phase
+    auto dma_chunk_k = [&](const Dma& d, int t) {
         dma16_untracked(d.src, doff[t], d.m0 + 1024 * (CPW * w + t));
     };
-    auto dma_last = [&](const Dma& d) {
+    auto dma_chunk_v = [&](const Dma& d, int t) {
+        if constexpr (CP == 1) dma16_untracked(d.src, doff[t], d.m0 + 1024 * (CPW * w + t));
+        else dma16_untracked(d.src, doffv[t], d.m0 + 1024 * (CPWV * w + t));
+    };
+    auto dma_last_k = [&](const Dma& d) {
         if (w == 0) dma16_untracked(d.src, doff[CPW], d.m0 + 1024 * (CHUNKS - 1));
+    };
+    auto dma_last_v = [&](const Dma& d) {
+        if constexpr (CP == 1) dma_last_k(d);
+        else if (w == 0) dma16_untracked(d.src, doffv[CPWV], d.m0 + 1024 * (CHUNKSV - 1));
     };
     auto issue = [&](int ph) {
         const Dma d = dma_setup(ph);
+        if (ph & 1) {
 #pragma unroll
-        for (int t = 0; t < CPW; ++t) dma_chunk(d, t);
-        dma_last(d);
+            for (int t = 0; t < CPWV; ++t) dma_chunk_v(d, t);
+            dma_last_v(d);
+        } else {
+#pragma unroll
+            for (int t = 0; t < CPW; ++t) dma_chunk_k(d, t);
+            dma_last_k(d);
+        }
     };
 
     // Q^T operand of the score unit's block, k-step s:
@@ -305,10 +347,10 @@ void flash16_kernel(Params p) {
 
     // Per-lane LDS read bases within a tile buffer (fragments differ by
     // immediate offsets): K row 16 kbo + j at byte 16 g (k-step s adds 64 s);
-    // V row 4g + e at byte 2 (d0 + 4q) for lane 16g + 4e + q (column block t
-    // adds 32 t, key half 16 rows).
+    // V row 4g + e at byte 2 (w DW + 4q) of the tile (the workgroup's columns)
+    // for lane 16g + 4e + q (column block t adds 32 t, key half 16 rows).
     const int kread = LROW * (16 * kbo + j) + 16 * g;
-    const int vread = LROW * (4 * g + (j >> 2)) + 2 * (d0 + 4 * (j & 3));
+    const int vread = LROWV * (4 * g + (j >> 2)) + 2 * (w * DW + 4 * (j & 3));
 
     if (tid == 0) restart_flag = 0;
 
@@ -328,6 +370,7 @@ void flash16_kernel(Params p) {
     f4 acc[NCB][DB];  // O^T[d0 + 16t + 4g + i][q0 + 16cl + j]
 
     XATTN_STAMP(clk_loop);
+    XATTN_CLOCK_DECL(pc_wait = 0, pc_qk = 0, pc_pv = 0);
     for (bool first = true;; first = false) {  // passes over the key range; a second is rare
         if (!first) issue(0);
         issue(1);
@@ -343,10 +386,13 @@ void flash16_kernel(Params p) {
             int ph = 2 * tile;
 
             // ---------------- scores of the owned unit over all of D ----------------
-            // K(t) has landed for every wavefront, and every wavefront is done
-            // with V(t - 1), whose buffer takes K(t + 1).
-            wait_vmcnt<CPW>();
+            // K(t) has landed for every wavefront (only this wavefront's chunks
+            // of V(t) may still be in flight), and every wavefront is done with
+            // V(t - 1), whose buffer takes K(t + 1).
+            XATTN_STAMP(pc_a);
+            wait_vmcnt<CPWV>();
             lds_barrier();
+            XATTN_STAMP(pc_b);
             f4 sacc[Sh::NCH];
 #pragma unroll
             for (int c = 0; c < Sh::NCH; ++c) sacc[c] = (f4){0.f, 0.f, 0.f, 0.f};
@@ -360,8 +406,8 @@ void flash16_kernel(Params p) {
                 for (int s = 0; s < KSF; ++s) {
                     if (s + KPF < KSF) kf[s + KPF] = *(const v8*)(kr + 64 * (s + KPF));
                     constexpr int KSTEP = KSF / CPW;  // one chunk per KSTEP k-steps
-                    if (s % KSTEP == 1) dma_chunk(dk, s / KSTEP);
-                    if (s == KSF - 1) dma_last(dk);
+                    if (s % KSTEP == 1) dma_chunk_k(dk, s / KSTEP);
+                    if (s == KSF - 1) dma_last_k(dk);
                     sacc[s % Sh::NCH] = mfma32<T>(kf[s], qr[s], sacc[s % Sh::NCH]);
                     __builtin_amdgcn_sched_barrier(0);
                 }
@@ -402,11 +448,14 @@ void flash16_kernel(Params p) {
                 (u2v){pack2<T>(pw[0], pw[1]), pack2<T>(pw[2], pw[3])};
 
             // ---------------- O^T += V^T . P^T over this wavefront's slice ----------------
-            // V(t) has landed, P is complete, and every wavefront is done with
-            // K(t), whose buffer takes V(t + 1).
+            // V(t) has landed (only this wavefront's chunks of K(t + 1) may
+            // still be in flight), P is complete, and every wavefront is done
+            // with K(t), whose buffer takes V(t + 1).
             ph += 1;
+            XATTN_STAMP(pc_c);
             wait_vmcnt<CPW>();
             lds_barrier();
+            XATTN_STAMP(pc_d);
             v8 pt[NCB];
 #pragma unroll
             for (int cl = 0; cl < NCB; ++cl)
@@ -418,17 +467,17 @@ void flash16_kernel(Params p) {
 #pragma unroll
                 for (int t = 0; t < VPF; ++t) {
                     va[t] = tr_read(vr + 4 * t);
-                    vc[t] = tr_read(vr + 2 * LROW + 4 * t);
+                    vc[t] = tr_read(vr + 2 * LROWV + 4 * t);
                 }
 #pragma unroll
                 for (int t = 0; t < DB; ++t) {
                     if (t + VPF < DB) {
                         va[t + VPF] = tr_read(vr + 4 * (t + VPF));
-                        vc[t + VPF] = tr_read(vr + 2 * LROW + 4 * (t + VPF));
+                        vc[t + VPF] = tr_read(vr + 2 * LROWV + 4 * (t + VPF));
                     }
-                    constexpr int VSTEP = DB / CPW;  // one chunk per VSTEP column blocks
-                    if (t % VSTEP == 0) dma_chunk(dv, t / VSTEP);
-                    if (t == DB - 1) dma_last(dv);
+                    constexpr int VSTEP = DB / CPWV;  // one chunk per VSTEP column blocks
+                    if (t % VSTEP == 0) dma_chunk_v(dv, t / VSTEP);
+                    if (t == DB - 1) dma_last_v(dv);
                     const v8 vt = __builtin_bit_cast(
                         v8, __builtin_shufflevector(va[t], vc[t], 0, 1, 2, 3, 4, 5, 6, 7));
 #pragma unroll
@@ -436,6 +485,11 @@ void flash16_kernel(Params p) {
                     __builtin_amdgcn_sched_barrier(0);
                 }
             }
+            XATTN_STAMP(pc_e);
+            XATTN_CLOCK_ADD(pc_wait, pc_a, pc_b);
+            XATTN_CLOCK_ADD(pc_wait, pc_c, pc_d);
+            XATTN_CLOCK_ADD(pc_qk, pc_b, pc_c);
+            XATTN_CLOCK_ADD(pc_pv, pc_d, pc_e);
         }
         // Every wavefront raises the flag (if at all) before this barrier, so
         // all of them read the same value.
@@ -476,7 +530,7 @@ void flash16_kernel(Params p) {
         const float factor = fast_exp2((sref[cb * QB + j] - mt) * kLog2e);
         const float l = s0.y + s1.y;
         rsc[cb] = PARTIAL ? factor : factor / (l * factor + 1e-6f);
-        if (PARTIAL && w == 0 && g == 0) {
+        if (PARTIAL && ch == 0 && w == 0 && g == 0) {
             const int q = q0 + QB * cb + j;
             if (q < p.NL) {
                 const size_t pi = ((size_t)b * p.NL + q) * p.S + split;
@@ -517,7 +571,7 @@ void flash16_kernel(Params p) {
     if (lane == 0 && blockIdx.x < (unsigned)kClockBlocks) {
         unsigned long long* c = phase_clock[blockIdx.x][w];
         c[0] = clk_start, c[1] = clk_loop, c[2] = clk_loop_end, c[3] = clk_end;
-        c[4] = rt_start, c[5] = rt_end, c[6] = c[7] = c[8] = 0;
+        c[4] = rt_start, c[5] = rt_end, c[6] = pc_wait, c[7] = pc_qk, c[8] = pc_pv;
     }
 #endif
 }
@@ -542,18 +596,21 @@ extern "C" int xattn_phase_clock_clear_f16(void) {
 #endif
 
 template <typename T, bool PARTIAL>
-static void launch16(int nw, dim3 grid, hipStream_t stream, const h16::Params& p) {
-    if (nw == 8)
-        hipLaunchKernelGGL((h16::flash16_kernel<T, PARTIAL, 8>), grid, dim3(8 * kWave), 0, stream, p);
+static void launch16(int nw, int cp, dim3 grid, hipStream_t stream, const h16::Params& p) {
+    if (nw == 4)
+        hipLaunchKernelGGL((h16::flash16_kernel<T, PARTIAL, 4, 1>), grid, dim3(4 * kWave), 0, stream, p);
+    else if (cp == 2)
+        hipLaunchKernelGGL((h16::flash16_kernel<T, PARTIAL, 8, 2>), grid, dim3(8 * kWave), 0, stream, p);
     else
-        hipLaunchKernelGGL((h16::flash16_kernel<T, PARTIAL, 4>), grid, dim3(4 * kWave), 0, stream, p);
+        hipLaunchKernelGGL((h16::flash16_kernel<T, PARTIAL, 8, 1>), grid, dim3(8 * kWave), 0, stream, p);
 }
 
-bool launch_flash16(bool bf16, int nw, const void* Q, const void* K, const void* V, float* out,
-                    float* po, float* pm, float* pl, int B, int NL, int NI, int S, int chunk,
-                    hipStream_t stream) {
-    if (nw != 4 && nw != 8) {
-        set_error(XATTN_ERR_INVALID_VALUE, "flash16: %d wavefronts per workgroup", nw);
+bool launch_flash16(bool bf16, int nw, int cp, const void* Q, const void* K, const void* V,
+                    float* out, float* po, float* pm, float* pl, int B, int NL, int NI, int S,
+                    int chunk, hipStream_t stream) {
+    if ((nw != 4 && nw != 8) || (cp != 1 && cp != 2) || (nw == 4 && cp != 1)) {
+        set_error(XATTN_ERR_INVALID_VALUE, "flash16: %d wavefronts per workgroup, %d column parts",
+                  nw, cp);
         return false;
     }
     h16::Params p;
@@ -561,7 +618,7 @@ bool launch_flash16(bool bf16, int nw, const void* Q, const void* K, const void*
     p.out = out; p.po = po; p.pm = pm; p.pl = pl;
     p.B = B; p.NL = NL; p.NI = NI; p.S = S; p.chunk = chunk;
     p.row_blocks = h16_row_blocks(NL, nw);
-    const long long nblk = (long long)B * p.row_blocks * S;
+    const long long nblk = (long long)B * p.row_blocks * S * cp;
     if (nblk <= 0) return true;
     if (nblk > 0x7fffffffLL) {
         set_error(XATTN_ERR_INVALID_VALUE, "grid of %lld workgroups too large", nblk);
@@ -569,11 +626,11 @@ bool launch_flash16(bool bf16, int nw, const void* Q, const void* K, const void*
     }
     const dim3 grid((unsigned)nblk);
     if (bf16) {
-        if (po) launch16<__bf16, true>(nw, grid, stream, p);
-        else launch16<__bf16, false>(nw, grid, stream, p);
+        if (po) launch16<__bf16, true>(nw, cp, grid, stream, p);
+        else launch16<__bf16, false>(nw, cp, grid, stream, p);
     } else {
-        if (po) launch16<_Float16, true>(nw, grid, stream, p);
-        else launch16<_Float16, false>(nw, grid, stream, p);
+        if (po) launch16<_Float16, true>(nw, cp, grid, stream, p);
+        else launch16<_Float16, false>(nw, cp, grid, stream, p);
     }
     return check_launch(bf16 ? "flash_bf16" : "flash_f16");
 }

@@ -28,10 +28,12 @@ bool launch_lse_combine(const float* po, const float* pm, const float* pl, float
 
 // fp16 / bf16 MFMA flash kernel; Q/K/V are 16-bit bit patterns, Q pre-scaled
 // by 1/sqrt(768).  Same po semantics as launch_flash_f32.  nw = 8: 64-latent
-// workgroups of 8 wavefronts; nw = 4: 32-latent workgroups of 4.
-bool launch_flash16(bool bf16, int nw, const void* Q, const void* K, const void* V, float* out,
-                    float* po, float* pm, float* pl, int B, int NL, int NI, int S, int chunk,
-                    hipStream_t stream);
+// workgroups of 8 wavefronts; nw = 4: 32-latent workgroups of 4.  cp = 2 (nw
+// = 8 only): each row block runs as two workgroups, one per half of the
+// output columns (each computes the block's scores over all of D).
+bool launch_flash16(bool bf16, int nw, int cp, const void* Q, const void* K, const void* V,
+                    float* out, float* po, float* pm, float* pl, int B, int NL, int NI, int S,
+                    int chunk, hipStream_t stream);
 int h16_row_blocks(int NL, int nw);
 
 // fp32 ladder rungs

@@ -147,6 +147,9 @@ lib.xattn_plan_splits.argtypes = [_I, _I, _I, _I, _I, _I]
 lib.xattn_plan_splits.restype = ctypes.c_int
 lib.xattn_wmma_plan.argtypes = [_I, _I, _I, _I, ctypes.POINTER(_I), ctypes.POINTER(_I)]
 lib.xattn_wmma_plan.restype = None
+lib.xattn_wmma_plan_ex.argtypes = [_I, _I, _I, _I, ctypes.POINTER(_I), ctypes.POINTER(_I),
+                                  ctypes.POINTER(_I)]
+lib.xattn_wmma_plan_ex.restype = None
 lib.xattn_f32_plan.argtypes = [_I, _I, _I, _I, ctypes.POINTER(_I), ctypes.POINTER(_I)]
 lib.xattn_f32_plan.restype = None
 lib.xattn_f32_split_latents.argtypes = [_I, _I, _I, _I, _I]
@@ -182,6 +185,16 @@ def wmma_plan(batch_size, N_latent, N_input, sm_count):
     lib.xattn_wmma_plan(batch_size, N_latent, N_input, int(sm_count), ctypes.byref(lpw),
                         ctypes.byref(s))
     return lpw.value, s.value
+
+
+def wmma_plan_form(batch_size, N_latent, N_input, sm_count):
+    """(latents per workgroup, column parts, key splits) of the same plan:
+    column parts 2 runs each 64-latent row block as two workgroups, one per
+    half of the output columns."""
+    lpw, cp, s = _I(0), _I(0), _I(0)
+    lib.xattn_wmma_plan_ex(batch_size, N_latent, N_input, int(sm_count), ctypes.byref(lpw),
+                           ctypes.byref(cp), ctypes.byref(s))
+    return lpw.value, cp.value, s.value
 
 
 def plan_num_splits(N_latent, N_input, batch_size, sm_count, keys_per_tile=KEYS_PER_TILE_F32):
@@ -221,6 +234,10 @@ HAS_SPLITK = _bind_optional("launch_splitk_kernel", _SPLITK_ARGS)
 HAS_WMMA_SPLITK = _bind_optional("launch_wmma_splitk_kernel", _WMMA_SPLITK_ARGS)
 HAS_WMMA_BF16 = _bind_optional("launch_wmma_bf16_kernel", _WMMA_ARGS)
 HAS_WMMA_SPLITK_BF16 = _bind_optional("launch_wmma_splitk_bf16_kernel", _WMMA_SPLITK_ARGS)
+# The 16-bit path with a caller-given plan (bf16 flag, Q, K, V, output, B, NL,
+# NI, dim, latents per workgroup, column parts, key splits, stream; additive,
+# for plan tuning).
+HAS_WMMA_PLAN = _bind_optional("launch_wmma_plan_kernel", [_I] + _WMMA_ARGS[:-1] + [_I, _I, _I, _P])
 # launch_optimized_kernel with its split partials in static device scratch:
 # for callers that cannot allocate (additive, no reference counterpart).
 HAS_NOALLOC = _bind_optional("launch_optimized_kernel_noalloc", [_F, _F, _F, _F, _I, _I, _I, _I,

@@ -136,6 +136,21 @@ void launch_wmma_splitk_bf16_kernel(const uint16_t* Q, const uint16_t* K,
                                     int dim, int num_splits,
                                     hipStream_t stream);
 
+/* No reference counterpart: launch_wmma_kernel (bf16 == 0) or
+ * launch_wmma_bf16_kernel (bf16 != 0) with the caller's launch plan instead
+ * of xattn_wmma_plan's, for plan tuning and for measuring the planner's cost
+ * model: latents_per_workgroup 64 (column_parts 1 or 2) or 32 (column_parts
+ * 1), num_splits key splits of whole 32-key tiles (1 .. ceil(N_input / 32);
+ * split partials in the stream's library workspace, as above).  Any other
+ * plan is refused with XATTN_ERR_INVALID_VALUE before anything is
+ * enqueued.  Results match the planned entry points' within the 16-bit
+ * tolerance (different splits round differently). */
+void launch_wmma_plan_kernel(int bf16, const uint16_t* Q, const uint16_t* K,
+                             const uint16_t* V, float* output, int batch_size,
+                             int N_latent, int N_input, int dim,
+                             int latents_per_workgroup, int column_parts,
+                             int num_splits, hipStream_t stream);
+
 /* ---- library status / device queries (additive) ----------------------- */
 
 enum {
@@ -198,9 +213,17 @@ int xattn_f32_split_latents(int batch_size, int N_latent, int N_input, int num_s
  * reference counterpart): latents per workgroup (64 on 8 wavefronts, or 32
  * on 4) and key splits (32-key tiles, whole tiles per split), chosen by a
  * cost model of the 16-bit kernel and the merge fitted to MI355X launches.
- * Writes the latents per workgroup and the number of key splits. */
+ * Writes the latents per workgroup and the number of key splits (the column
+ * parts of 64-latent plans: xattn_wmma_plan_ex). */
 void xattn_wmma_plan(int batch_size, int N_latent, int N_input, int cu_count,
                      int* latents_per_workgroup, int* num_splits);
+/* The same plan with its third coordinate (no reference counterpart):
+ * column_parts 2 means each row block of 64 latents runs as two workgroups,
+ * one per half of the 768 output columns, both computing the block's scores
+ * over all of dim. */
+void xattn_wmma_plan_ex(int batch_size, int N_latent, int N_input, int cu_count,
+                        int* latents_per_workgroup, int* column_parts,
+                        int* num_splits);
 /* Latents per workgroup launch_wmma_splitk_kernel and its bf16 twin use for
  * num_splits key splits (64 or 32, by the cost model of xattn_wmma_plan; no
  * reference counterpart). */

@@ -17,5 +17,6 @@ int xattn_optimized_num_splits(void) { return 1; }
 int xattn_plan_splits(void) { return 1; }
 void xattn_f32_plan(void) {}
 void xattn_wmma_plan(void) {}
+void xattn_wmma_plan_ex(void) {}
 int xattn_f32_split_latents(void) { return 64; }
 int xattn_wmma_split_latents(void) { return 64; }

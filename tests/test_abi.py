@@ -106,29 +106,32 @@ def test_f32_plan(cw):
 
 
 def test_wmma_plan(cw):
-    # (latents per workgroup, key splits) of launch_wmma_kernel on 256 CUs.
-    # Where marked, the pair is the fastest of 2 workgroup sizes x 2-5 split
-    # counts timed on an MI355X at that shape; the others are the model's
-    # choice between timed neighbours within 4 %.
-    assert cw.wmma_plan(32, 1024, 784, 256) == (64, 1)   # measured best
-    assert cw.wmma_plan(16, 512, 784, 256) == (32, 1)    # measured best
-    assert cw.wmma_plan(8, 512, 784, 256) == (32, 2)     # measured best
-    assert cw.wmma_plan(4, 1024, 784, 256) == (32, 2)    # measured best
-    assert cw.wmma_plan(1, 256, 784, 256) == (32, 13)    # 1.6 % behind (32, 7)
-    assert cw.wmma_plan(1, 64, 784, 256) == (32, 13)     # measured best
-    assert cw.wmma_plan(2, 256, 4096, 256) == (32, 16)   # measured best
-    assert cw.wmma_plan(1, 512, 16384, 256) == (64, 32)  # measured best
-    assert cw.wmma_plan(1, 256, 50176, 256) == (64, 63)  # 25-tile chunks, as 64 splits give
-    assert cw.wmma_plan(1, 256, 4096, 256) == (32, 26)   # between (32, 16) and (32, 32)
-    assert cw.wmma_plan(1, 64, 20, 256) == (32, 1)       # one tile: nothing to split
+    # (latents per workgroup, column parts, key splits) of launch_wmma_kernel
+    # on 256 CUs.  Where marked, the plan is the fastest of every form and
+    # split count timed at that shape on an MI355X (wmma_plan_campaign.py);
+    # the others are within the spread of repeated timings of one plan.
+    form = cw.wmma_plan_form
+    assert form(32, 1024, 784, 256) == (64, 1, 1)   # measured best
+    assert form(16, 512, 784, 256) == (32, 1, 1)    # measured best
+    assert form(8, 1024, 784, 256) == (32, 1, 1)    # measured best
+    assert form(8, 512, 784, 256) == (64, 2, 1)     # measured best
+    assert form(4, 1024, 784, 256) == (64, 2, 1)    # measured best
+    assert form(16, 256, 784, 256) == (64, 2, 1)    # measured best
+    assert form(1, 64, 784, 256) == (64, 2, 13)     # measured best
+    assert form(1, 256, 4096, 256) == (64, 2, 22)   # measured best
+    assert form(1, 256, 784, 256) == (64, 2, 9)     # 4 % behind (64, 2, 7)
+    assert form(2, 256, 50176, 256) == (64, 1, 32)  # 1.3 % behind (64, 2, 16)
+    assert form(1, 64, 20, 256) == (64, 2, 1)       # one tile: nothing to split
+    for b, nl, ni in [(32, 1024, 784), (1, 256, 4096), (1, 64, 20)]:
+        assert cw.wmma_plan(b, nl, ni, 256) == (form(b, nl, ni, 256)[0], form(b, nl, ni, 256)[2])
     split = cw.lib.xattn_wmma_split_latents
     assert split(1, 256, 50176, 64, 256) == 64
-    assert split(1, 256, 4096, 32, 256) == 32
+    assert split(16, 512, 784, 1, 256) == 32
     for b, nl, ni in [(1, 1, 1), (2, 100, 33), (3, 7, 5000), (64, 64, 784), (1, 256, 4096),
                       (16, 512, 784)]:
-        lpw, s = cw.wmma_plan(b, nl, ni, 256)
+        lpw, cp, s = form(b, nl, ni, 256)
         tiles = -(-ni // 32)
-        assert lpw in (32, 64) and 1 <= s <= tiles
+        assert (lpw, cp) in ((64, 1), (64, 2), (32, 1)) and 1 <= s <= tiles
         ct = -(-tiles // s)
         assert -(-tiles // ct) == s  # whole-tile chunks leave no empty split
         # the split-K entry with the planned splits and the same chunk picks
@@ -136,6 +139,29 @@ def test_wmma_plan(cw):
         chunk = -(-(-(-ni // s)) // 16) * 16
         if -(-min(chunk, ni) // 32) == ct:
             assert split(b, nl, ni, s, 256) == lpw
+
+
+def test_wmma_plan_launch_refuses_other_plans(cw):
+    """launch_wmma_plan_kernel takes the three forms only and whole-tile
+    split counts 1..ceil(N_input / 32); anything else is refused before any
+    HIP call (so no GPU is needed to see it)."""
+    P = ctypes.c_void_p
+    F = ctypes.POINTER(ctypes.c_float)
+    dummy = ctypes.cast(P(0x1000), F)
+    q = P(0x1000)
+    s0 = P(0)
+    for lpw, cp, s in [(16, 1, 1), (32, 2, 1), (64, 3, 1), (64, 1, 0), (64, 2, 26), (32, 1, -1)]:
+        code, msg = _call(cw, "launch_wmma_plan_kernel", 1, q, q, q, dummy, 1, 64, 784, 768,
+                          lpw, cp, s, s0)
+        assert code == 1, (lpw, cp, s, msg)
+        assert ("column parts" in msg) if s >= 1 and s <= 25 else ("num_splits" in msg), msg
+    code, msg = _call(cw, "launch_wmma_plan_kernel", 0, q, q, q, dummy, 1, 64, 784, 100,
+                      64, 1, 1, s0)
+    assert code == 2 and "dim=100" in msg
+    # an empty problem is a no-op, whatever the (valid) plan
+    code, _ = _call(cw, "launch_wmma_plan_kernel", 0, q, q, q, dummy, 0, 64, 784, 768, 64, 2, 3,
+                    s0)
+    assert code == 0
 
 
 def test_split_drivers_default_to_the_reference_heuristic(cw):

@@ -105,3 +105,21 @@ def test_phase_clock_needs_the_instrumented_library():
         bench.phase_clock(NoClock(), "headline-bf16")
     with pytest.raises(RuntimeError, match="no phase-clock stamps"):
         bench.phase_clock(_FakeCw(lambda c: c.fill(0)), "cfg1")
+
+
+def test_plan_option():
+    """--plan LPW/CP/S parses into the three numbers, and an fp32 case
+    refuses it before touching the device."""
+    import argparse
+
+    import pytest
+
+    sys.path.insert(0, ROOT)
+    import bench
+    assert bench.parse_plan("64/2/1") == (64, 2, 1)
+    assert bench.parse_plan("32/1/13") == (32, 1, 13)
+    for bad in ("64/2", "a/b/c", "64-2-1"):
+        with pytest.raises(argparse.ArgumentTypeError):
+            bench.parse_plan(bad)
+    with pytest.raises(ValueError, match="16-bit"):
+        bench.run_case(None, "cfg1", 1, 1, plan=(64, 1, 1))

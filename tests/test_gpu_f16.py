@@ -7,6 +7,7 @@ kernel's own error (P rounded to 16 bits, fp32 accumulation):
 rel <= 4e-3 for bf16 and <= 1e-3 for fp16.
 """
 
+import ctypes
 import math
 
 import numpy as np
@@ -77,6 +78,40 @@ def test_bitwise_repeatable(cw, oracle, bf16, b, nl, ni, s):
             assert np.array_equal(x, y)
     assert np.array_equal(a, c)
     _check(oracle, cw, a, q, k, v, bf16)
+
+
+def _run_plan(cw, q, k, v, bf16, lpw, cp, s):
+    """One launch_wmma_plan_kernel call with the given plan; the output."""
+    b, nl, d = q.shape
+    ni = k.shape[1]
+    bufs = [cw.DeviceBuffer.holding(a) for a in cw._half_inputs(q, k, v, b, d, bf16)]
+    out = cw.DeviceBuffer(b * nl * d * 4).zero()
+    try:
+        cw.lib.launch_wmma_plan_kernel(int(bf16), *[p.ptr for p in bufs], out.f32, b, nl, ni, d,
+                                       lpw, cp, s, ctypes.c_void_p(0))
+        cw._lib_error_check("launch_wmma_plan_kernel")
+        assert cw.cudart.cudaDeviceSynchronize() == 0
+        return out.download((b, nl, d))
+    finally:
+        for p in bufs + [out]:
+            p.close()
+
+
+@pytest.mark.parametrize("bf16", [False, True], ids=["fp16", "bf16"])
+@pytest.mark.parametrize("lpw,cp", [(64, 1), (64, 2), (32, 1)], ids=["64", "64x2cols", "32"])
+@pytest.mark.parametrize("s", [1, 3, 7])
+def test_every_plan_form(cw, oracle, bf16, lpw, cp, s):
+    """Each workgroup form the planner may pick (64 latents, 64 latents in
+    two column halves, 32 latents), unsplit and split, on a ragged shape
+    (latents past the last full block, a partial last key tile), checked
+    against the oracle.  Unsplit, the column halves give the full-width
+    form's bits (the same scores, weights and MFMAs per output column)."""
+    b, nl, ni = 2, 80, 200
+    q, k, v = oracle.make_inputs(b, nl, ni, 768, seed=41)
+    out = _run_plan(cw, q, k, v, bf16, lpw, cp, s)
+    _check(oracle, cw, out, q, k, v, bf16)
+    if s == 1 and cp == 2:
+        assert np.array_equal(out, _run_plan(cw, q, k, v, bf16, 64, 1, 1))
 
 
 @pytest.mark.parametrize("bf16", [False, True], ids=["fp16", "bf16"])
