@@ -365,7 +365,7 @@ constexpr H16Form kH16Forms[] = {{8, 1}, {8, 2}, {4, 1}};
 // 32-key tiles each, fitted (least squares on relative error) to 582 timed
 // bf16 launches on MI355X: every form and split count the planner weighs at
 // 27 shapes, B = 1..32, N_latent = 64..1024, N_input = 784..50176
-// (experiments/wmma_plan_campaign.py, experiments/fit_wmma_cost.py).  Per
+// (experiments/plan_campaign.py, experiments/fit_plan_cost.py).  Per
 // launch 3.22 µs; per round of workgroups, a 32-key tile costs 1.67 µs at 64
 // latents, 1.08 µs at 64 latents and half the columns, 1.22 µs at 32
 // latents, and 0.22 / 0.34 / 0.19 µs more when an unsplit launch fills every
@@ -591,16 +591,12 @@ void launch_tiled_kernel(const float* Q, const float* K, const float* V, float* 
     launch_tiled(Q, K, V, output, batch_size, N_latent, N_input, dim, stream);
 }
 
-void launch_optimized_kernel(const float* Q, const float* K, const float* V, float* output,
-                             int batch_size, int N_latent, int N_input, int dim,
-                             hipStream_t stream) {
-    const char* who = "launch_optimized_kernel";
-    if (!validate_common(who, Q, K, V, output, batch_size, N_latent, N_input, dim)) return;
-    if (!validate_dim768(who, dim)) return;
-    if (!validate_aligned16(who, Q, K, V, output, nullptr)) return;
-    if (batch_size == 0 || N_latent == 0) return;
-    int ds = 1, S = 1;
-    f32_plan(batch_size, N_latent, N_input, device_cu_count(), &ds, &S);
+// An fp32 launch with a given plan: ds wavefronts per 16-latent block
+// (64 / ds latents per workgroup), S key splits of whole 16-key tiles
+// (partials in the stream's library workspace when S > 1).
+static void optimized_run(const float* Q, const float* K, const float* V, float* output,
+                          int batch_size, int N_latent, int N_input, int ds, int S,
+                          hipStream_t stream) {
     if (S <= 1) {
         launch_flash_f32(ds, Q, K, V, output, nullptr, nullptr, nullptr, batch_size, N_latent,
                          N_input, 1, N_input, stream);
@@ -615,6 +611,44 @@ void launch_optimized_kernel(const float* Q, const float* K, const float* V, flo
                          N_input, S, chunk, stream))
         launch_lse_combine(sc.po, sc.pm, sc.pl, output, batch_size * N_latent, S, stream);
     lease.release();
+}
+
+void launch_optimized_kernel(const float* Q, const float* K, const float* V, float* output,
+                             int batch_size, int N_latent, int N_input, int dim,
+                             hipStream_t stream) {
+    const char* who = "launch_optimized_kernel";
+    if (!validate_common(who, Q, K, V, output, batch_size, N_latent, N_input, dim)) return;
+    if (!validate_dim768(who, dim)) return;
+    if (!validate_aligned16(who, Q, K, V, output, nullptr)) return;
+    if (batch_size == 0 || N_latent == 0) return;
+    int ds = 1, S = 1;
+    f32_plan(batch_size, N_latent, N_input, device_cu_count(), &ds, &S);
+    optimized_run(Q, K, V, output, batch_size, N_latent, N_input, ds, S, stream);
+}
+
+void launch_optimized_plan_kernel(const float* Q, const float* K, const float* V,
+                                  float* output, int batch_size, int N_latent, int N_input,
+                                  int dim, int latents_per_workgroup, int num_splits,
+                                  hipStream_t stream) {
+    const char* who = "launch_optimized_plan_kernel";
+    if (!validate_common(who, Q, K, V, output, batch_size, N_latent, N_input, dim)) return;
+    if (!validate_dim768(who, dim)) return;
+    if (!validate_aligned16(who, Q, K, V, output, nullptr)) return;
+    if (latents_per_workgroup != 64 && latents_per_workgroup != 32 &&
+        latents_per_workgroup != 16) {
+        set_error(XATTN_ERR_INVALID_VALUE, "%s: %d latents per workgroup (64, 32 or 16)", who,
+                  latents_per_workgroup);
+        return;
+    }
+    const int tiles = (N_input + 15) / 16;
+    if (num_splits < 1 || num_splits > std::max(tiles, 1)) {
+        set_error(XATTN_ERR_INVALID_VALUE, "%s: num_splits %d outside 1..%d (16-key tiles)", who,
+                  num_splits, std::max(tiles, 1));
+        return;
+    }
+    if (batch_size == 0 || N_latent == 0) return;
+    optimized_run(Q, K, V, output, batch_size, N_latent, N_input, 64 / latents_per_workgroup,
+                  N_input == 0 ? 1 : num_splits, stream);
 }
 
 void launch_optimized_kernel_noalloc(const float* Q, const float* K, const float* V,

@@ -238,6 +238,10 @@ HAS_WMMA_SPLITK_BF16 = _bind_optional("launch_wmma_splitk_bf16_kernel", _WMMA_SP
 # NI, dim, latents per workgroup, column parts, key splits, stream; additive,
 # for plan tuning).
 HAS_WMMA_PLAN = _bind_optional("launch_wmma_plan_kernel", [_I] + _WMMA_ARGS[:-1] + [_I, _I, _I, _P])
+# launch_optimized_kernel with a caller-given plan (Q, K, V, output, B, NL, NI,
+# dim, latents per workgroup, key splits, stream; additive, for plan tuning).
+HAS_OPTIMIZED_PLAN = _bind_optional("launch_optimized_plan_kernel",
+                                    [_F, _F, _F, _F, _I, _I, _I, _I, _I, _I, _P])
 # launch_optimized_kernel with its split partials in static device scratch:
 # for callers that cannot allocate (additive, no reference counterpart).
 HAS_NOALLOC = _bind_optional("launch_optimized_kernel_noalloc", [_F, _F, _F, _F, _I, _I, _I, _I,

@@ -1,12 +1,14 @@
 """
-Fits the 16-bit planner's cost model (csrc/xattn_abi.hip, h16_cost) to the
-timings experiments/wmma_plan_campaign.py writes, and reports how well the
-fitted model and the library's own plans pick among the timed plans.
+Fits a planner's cost model (csrc/xattn_abi.hip: f32_cost for the fp32
+path, h16_cost for the 16-bit one) to the timings
+experiments/plan_campaign.py writes, and reports how well the fitted model
+and the library's own plans pick among the timed plans.
 
-    python fast-cuda-cross-attention_amd/experiments/fit_wmma_cost.py plans.jsonl
+    python fast-cuda-cross-attention_amd/experiments/fit_plan_cost.py plans.jsonl
 
 Model, for a launch of W workgroups (B * row blocks * splits * column
-parts) in R = ceil(W / CUs) rounds of ct 32-key tiles each:
+parts) in R = ceil(W / CUs) rounds of ct key tiles each (16 keys fp32, 32
+keys 16-bit):
 
     t = c0 + R * (r0 + ct * (tile[form] + full[form] * [S == 1 and W >= CUs]))
           + [S > 1] * (m0 + m1 * MB of partials + m2 * S * max(0, 1 - B*NL / CUs))
@@ -22,22 +24,32 @@ from scipy.optimize import lsq_linear
 
 CU = 256
 D = 768
-FORMS = [(64, 1), (64, 2), (32, 1)]
-NAMES = (["c0", "r0"] + [f"tile{f}" for f in FORMS] + [f"full{f}" for f in FORMS]
-         + ["m0", "m1_per_MB", "m2"])
+# workgroup forms (latents per workgroup, column parts) and key-tile size
+FORMS = {"fp32": [(64, 1), (32, 1), (16, 1)], "16bit": [(64, 1), (64, 2), (32, 1)]}
+TILE = {"fp32": 16, "16bit": 32}
+
+
+def path_of(r):
+    return "fp32" if r.get("dtype") == "fp32" else "16bit"
+
+
+def names(path):
+    return (["c0", "r0"] + [f"tile{f}" for f in FORMS[path]] + [f"full{f}" for f in FORMS[path]]
+            + ["m0", "m1_per_MB", "m2"])
 
 
 def features(r):
+    path = path_of(r)
     f = (r["lpw"], r["cp"])
     rows_blk = (r["NL"] + r["lpw"] - 1) // r["lpw"]
     w = r["B"] * rows_blk * r["S"] * r["cp"]
     rounds = -(-w // CU)
-    tiles = (r["NI"] + 31) // 32
+    tiles = (r["NI"] + TILE[path] - 1) // TILE[path]
     ct = -(-tiles // r["S"])
     full = r["S"] == 1 and w >= CU
     x = [1.0, float(rounds)]
-    x += [rounds * ct if g == f else 0.0 for g in FORMS]
-    x += [rounds * ct if (g == f and full) else 0.0 for g in FORMS]
+    x += [rounds * ct if g == f else 0.0 for g in FORMS[path]]
+    x += [rounds * ct if (g == f and full) else 0.0 for g in FORMS[path]]
     split = r["S"] > 1
     rows = r["B"] * r["NL"]
     x += [1.0 if split else 0.0, rows * r["S"] * D * 4e-6 if split else 0.0,
@@ -60,8 +72,11 @@ def main():
     timed = [r for r in rows if not r.get("planned")]
     planned = {shape_of(r): r for r in rows if r.get("planned")}
     shapes = sorted(set(shape_of(r) for r in timed))
+    paths = set(path_of(r) for r in timed)
+    if len(paths) != 1:
+        raise SystemExit("one path (fp32 or 16-bit) per file")
     p = fit(timed)
-    print("coefficients:", ", ".join(f"{n} {v:.3f}" for n, v in zip(NAMES, p)))
+    print("coefficients:", ", ".join(f"{n} {v:.3f}" for n, v in zip(names(paths.pop()), p)))
 
     def loss_table(params, label, show):
         losses = []

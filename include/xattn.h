@@ -75,6 +75,19 @@ void launch_optimized_kernel(const float* Q, const float* K, const float* V,
                              float* output, int batch_size, int N_latent,
                              int N_input, int dim, hipStream_t stream);
 
+/* No reference counterpart: launch_optimized_kernel with the caller's
+ * launch plan instead of xattn_f32_plan's, for plan tuning and for
+ * measuring the planner's cost model: latents_per_workgroup 64, 32 or 16,
+ * num_splits key splits of whole 16-key tiles (1 .. ceil(N_input / 16);
+ * split partials in the stream's library workspace).  Any other plan is
+ * refused with XATTN_ERR_INVALID_VALUE before anything is enqueued.  Results
+ * match launch_optimized_kernel's within the fp32 tolerance (different
+ * splits and workgroup sizes sum in different orders). */
+void launch_optimized_plan_kernel(const float* Q, const float* K, const float* V,
+                                  float* output, int batch_size, int N_latent,
+                                  int N_input, int dim, int latents_per_workgroup,
+                                  int num_splits, hipStream_t stream);
+
 /* No counterpart in the reference: launch_optimized_kernel for callers that
  * cannot allocate device memory (code under HIP graph capture, tight
  * serving loops, harnesses that forbid hipMalloc).  Same plan, kernels and

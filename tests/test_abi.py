@@ -108,7 +108,7 @@ def test_f32_plan(cw):
 def test_wmma_plan(cw):
     # (latents per workgroup, column parts, key splits) of launch_wmma_kernel
     # on 256 CUs.  Where marked, the plan is the fastest of every form and
-    # split count timed at that shape on an MI355X (wmma_plan_campaign.py);
+    # split count timed at that shape on an MI355X (plan_campaign.py);
     # the others are within the spread of repeated timings of one plan.
     form = cw.wmma_plan_form
     assert form(32, 1024, 784, 256) == (64, 1, 1)   # measured best
@@ -225,6 +225,24 @@ def _call(cw, name, *args):
     fn = getattr(cw.lib, name)
     fn(*args)
     return cw.lib.xattn_get_last_error(), cw.lib.xattn_get_last_error_string().decode()
+
+
+def test_optimized_plan_launch_refuses_other_plans(cw):
+    """launch_optimized_plan_kernel takes 64, 32 or 16 latents per workgroup
+    and whole-tile split counts 1..ceil(N_input / 16) only, refused before
+    any HIP call."""
+    F = ctypes.POINTER(ctypes.c_float)
+    dummy = ctypes.cast(ctypes.c_void_p(0x1000), F)
+    s0 = ctypes.c_void_p(0)
+    for lpw, s, what in [(8, 1, "latents"), (48, 1, "latents"), (64, 0, "num_splits"),
+                         (16, 50, "num_splits"), (32, -2, "num_splits")]:
+        code, msg = _call(cw, "launch_optimized_plan_kernel", dummy, dummy, dummy, dummy, 1, 64,
+                          784, 768, lpw, s, s0)
+        assert code == 1 and what in msg, (lpw, s, msg)
+    # an empty problem is a no-op, whatever the (valid) plan
+    code, _ = _call(cw, "launch_optimized_plan_kernel", dummy, dummy, dummy, dummy, 1, 0, 784,
+                    768, 16, 49, s0)
+    assert code == 0
 
 
 def test_noalloc_refuses_plans_past_its_scratch(cw):

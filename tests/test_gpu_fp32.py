@@ -6,6 +6,8 @@ experiments/bench_perceiver_ni.py:147-148).  Every case calls the HIP library
 through its C ABI (cuda_wrappers -> kernels.so).
 """
 
+import ctypes
+
 import numpy as np
 import pytest
 
@@ -48,6 +50,28 @@ def test_headline_shape_and_determinism(cw, oracle):
 def test_edge_shapes(cw, oracle, b, nl, ni):
     q, k, v = oracle.make_inputs(b, nl, ni, 768, seed=b * 1000 + nl + ni)
     fp32_gate(_events(cw, "vectorized", q, k, v), oracle.attention_f64(q, k, v))
+
+
+@pytest.mark.parametrize("lpw", [64, 32, 16])
+@pytest.mark.parametrize("s", [1, 3, 7])
+def test_every_plan_form(cw, oracle, lpw, s):
+    """Each workgroup size the planner may pick (64, 32 or 16 latents),
+    unsplit and split, through launch_optimized_plan_kernel on a ragged
+    shape (latents past the last full block, a partial last key tile)."""
+    b, nl, ni = 2, 80, 200
+    q, k, v = oracle.make_inputs(b, nl, ni, 768, seed=43)
+    bufs = [cw.DeviceBuffer.holding(a) for a in (q, k, v)]
+    out = cw.DeviceBuffer(b * nl * 768 * 4).zero()
+    try:
+        cw.lib.launch_optimized_plan_kernel(*[p.f32 for p in bufs], out.f32, b, nl, ni, 768, lpw,
+                                            s, ctypes.c_void_p(0))
+        cw._lib_error_check("launch_optimized_plan_kernel")
+        assert cw.cudart.cudaDeviceSynchronize() == 0
+        res = out.download((b, nl, 768))
+    finally:
+        for p in bufs + [out]:
+            p.close()
+    fp32_gate(res, oracle.attention_f64(q, k, v))
 
 
 def test_empty_key_set_gives_zeros(cw, oracle):

@@ -14,7 +14,7 @@ import pytest
 from conftest import PKG, ROOT
 
 FLAGS = ["HAS_WMMA", "HAS_SPLITK", "HAS_WMMA_SPLITK", "HAS_WMMA_BF16",
-         "HAS_WMMA_SPLITK_BF16", "HAS_NOALLOC", "HAS_WMMA_PLAN"]
+         "HAS_WMMA_SPLITK_BF16", "HAS_NOALLOC", "HAS_WMMA_PLAN", "HAS_OPTIMIZED_PLAN"]
 
 
 def _import_in_child(env_so, cwd):
