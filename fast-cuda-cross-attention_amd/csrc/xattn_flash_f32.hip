@@ -411,13 +411,15 @@ void flash_f32_kernel(Params p) {
 
 // Log-sum-exp merge of split partials (kernel_splitk.cu:186-236).  One
 // workgroup per (batch, latent) row, in P groups of 192 threads: every wave
-// first reduces M = max pm and L = sum exp(pm - M) pl over the splits
-// (lane-strided), then thread c of group p accumulates float4 column c over
-// splits p, p + P, ... with 8 partial rows in flight at a time, and the P
-// group sums are added in group order through LDS.  P = 1 when there are
-// enough rows to fill the device (HBM-bound: S * 3 KiB of po per row); P = 4
-// for fewer rows, where one group's chain of dependent loads would set the
-// time.
+// reduces M = max pm and L = sum exp(pm - M) pl over the splits
+// (lane-strided), and thread c of group p accumulates float4 column c over
+// splits p, p + P, ... with 8 partial rows in flight at a time; the P group
+// sums are added in group order through LDS.  The first 8 partial rows and
+// each lane's first pm / pl are requested before the reductions (the
+// partials do not depend on M), so a row with few splits waits for one
+// round of loads, not three.  P = 1 when there are enough rows to fill the
+// device (HBM-bound: S * 3 KiB of po per row); P = 4 for fewer rows, where
+// one group's chain of dependent loads would set the time.
 constexpr int kCombineThreads = kDim / 4;  // 192 threads per group
 
 template <int P>
@@ -431,33 +433,43 @@ void lse_combine_kernel(const float* __restrict__ po, const float* __restrict__ 
     const int grp = threadIdx.x / kCombineThreads;
     const float* pmr = pm + row * S;
     const float* plr = pl + row * S;
-
-    float M = -FLT_MAX;
-    for (int s = lane; s < S; s += kWave) M = fmaxf(M, pmr[s]);
-    M = wave_max(M);
-    float L = 0.f;
-    for (int s = lane; s < S; s += kWave) {
-        const float m = pmr[s];
-        if (m > -FLT_MAX) L += expf(m - M) * plr[s];
-    }
-    L = wave_sum(L);
+    const f4* src = (const f4*)(po + row * S * kDim) + c;
 
     // Batches of 8 splits per thread; a partial last batch re-reads split
     // S - 1 with weight 0, so every batch issues its 8 loads before the first
     // use (no chain of dependent single loads).
-    const f4* src = (const f4*)(po + row * S * kDim) + c;
-    f4 acc = {0.f, 0.f, 0.f, 0.f};
-    for (int s = grp; s < S; s += 8 * P) {
-        f4 v[8];
-        float wgt[8];
+    f4 v[8];
+    float mv[8];
+    auto load_batch = [&](int s) {
 #pragma unroll
         for (int u = 0; u < 8; ++u) {
             const int i = s + u * P;
             const int ic = i < S ? i : S - 1;
             v[u] = src[(size_t)ic * (kDim / 4)];
-            const float m = pmr[ic];
-            wgt[u] = (i >= S || m == -FLT_MAX) ? 0.f : expf(m - M);
+            mv[u] = pmr[ic];
         }
+    };
+    if (grp < S) load_batch(grp);
+    const float m_first = lane < S ? pmr[lane] : -FLT_MAX;
+    const float l_first = lane < S ? plr[lane] : 0.f;
+
+    float M = m_first;
+    for (int s = lane + kWave; s < S; s += kWave) M = fmaxf(M, pmr[s]);
+    M = wave_max(M);
+    float L = m_first > -FLT_MAX ? expf(m_first - M) * l_first : 0.f;
+    for (int s = lane + kWave; s < S; s += kWave) {
+        const float m = pmr[s];
+        if (m > -FLT_MAX) L += expf(m - M) * plr[s];
+    }
+    L = wave_sum(L);
+
+    f4 acc = {0.f, 0.f, 0.f, 0.f};
+    for (int s = grp; s < S; s += 8 * P) {
+        if (s != grp) load_batch(s);
+        float wgt[8];
+#pragma unroll
+        for (int u = 0; u < 8; ++u)
+            wgt[u] = (s + u * P >= S || mv[u] == -FLT_MAX) ? 0.f : expf(mv[u] - M);
 #pragma unroll
         for (int u = 0; u < 8; ++u) acc += wgt[u] * v[u];
     }
