@@ -417,9 +417,9 @@ void flash_f32_kernel(Params p) {
 // sums are added in group order through LDS.  The first 8 partial rows and
 // each lane's first pm / pl are requested before the reductions (the
 // partials do not depend on M), so a row with few splits waits for one
-// round of loads, not three.  P = 1 when there are enough rows to fill the
-// device (HBM-bound: S * 3 KiB of po per row); P = 4 for fewer rows, where
-// one group's chain of dependent loads would set the time.
+// round of loads, not three.  P = 1 when there are rows enough to fill the
+// device twice (HBM-bound: S * 3 KiB of po per row); P = 4 for fewer rows,
+// where one group's loads in flight would set the time.
 constexpr int kCombineThreads = kDim / 4;  // 192 threads per group
 
 template <int P>
@@ -542,7 +542,7 @@ bool launch_flash_f32(int ds, const float* Q, const float* K, const float* V, fl
 bool launch_lse_combine(const float* po, const float* pm, const float* pl, float* out,
                         int rows, int S, hipStream_t stream) {
     if (rows <= 0) return true;
-    if (rows < device_cu_count() && S > 1)
+    if (rows < 2 * device_cu_count() && S > 1)
         hipLaunchKernelGGL(f32::lse_combine_kernel<4>, dim3(rows), dim3(4 * f32::kCombineThreads),
                            0, stream, po, pm, pl, out, S);
     else
