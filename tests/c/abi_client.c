@@ -1,8 +1,9 @@
 /*
  * A C program that uses kernels.so through include/xattn.h alone (no Python,
- * no torch): the fp32 entry point, split-K with caller-owned scratch, and the
- * bf16 entry point on a small ragged problem, each checked against a
- * double-precision softmax(Q K^T / sqrt(D)) V computed here.
+ * no torch): the fp32 entry point, split-K with caller-owned scratch, the
+ * bf16 entry point and the two plan-override entry points on a small ragged
+ * problem, each checked against a double-precision softmax(Q K^T / sqrt(D)) V
+ * computed here.
  *
  *   gcc -std=c11 -D__HIP_PLATFORM_AMD__ -I/opt/rocm/include -Iinclude \
  *       tests/c/abi_client.c -L<dir of kernels.so> -l:kernels.so \
@@ -158,6 +159,20 @@ int main(void) {
     fails += status("launch_wmma_bf16_kernel");
     HIP_OK(hipMemcpy(out, dout, nq * 4, hipMemcpyDeviceToHost));
     fails += check("launch_wmma_bf16_kernel", out, ref, 1.0, 2e-2);
+
+    /* the plan-override entry points with plans of their own choosing:
+     * 64 latents in two column halves, 3 key splits (bf16); 16 latents, 5
+     * splits (fp32) */
+    HIP_OK(hipMemset(dout, 0, nq * 4));
+    launch_wmma_plan_kernel(1, bq, bk, bv, dout, B, NL, NI, D, 64, 2, 3, NULL);
+    fails += status("launch_wmma_plan_kernel");
+    HIP_OK(hipMemcpy(out, dout, nq * 4, hipMemcpyDeviceToHost));
+    fails += check("launch_wmma_plan_kernel", out, ref, 1.0, 2e-2);
+    HIP_OK(hipMemset(dout, 0, nq * 4));
+    launch_optimized_plan_kernel(dq, dk, dv, dout, B, NL, NI, D, 16, 5, NULL);
+    fails += status("launch_optimized_plan_kernel");
+    HIP_OK(hipMemcpy(out, dout, nq * 4, hipMemcpyDeviceToHost));
+    fails += check("launch_optimized_plan_kernel", out, ref, 1e-4, 1e-3);
 
     /* an argument the kernels cannot run with is refused, not launched */
     launch_optimized_kernel(dq, dk, dv, dout, B, NL, NI, 64, NULL);
