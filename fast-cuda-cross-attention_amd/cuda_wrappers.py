@@ -742,6 +742,44 @@ def benchmark_wmma_splitk_bf16_events(Q, K, V, batch_size, N_latent, N_input, D,
     return out, mean_ms, std_ms, s
 
 
+def benchmark_plan_events(Q, K, V, batch_size, N_latent, N_input, D, latents_per_workgroup,
+                          num_splits, column_parts=1, precision="fp32", warmup=20, iters=100):
+    """Event timing of the fused path under a given launch plan instead of
+    the library's (additive, for plan tuning): launch_optimized_plan_kernel
+    for precision "fp32" (64, 32 or 16 latents per workgroup), else
+    launch_wmma_plan_kernel ("fp16" or "bf16"; 64 latents in one or two
+    column parts, or 32).  Returns (output, mean_ms, std_ms); a plan the
+    library refuses raises RuntimeError before anything is timed."""
+    _require_dim(D, "the MFMA kernels")
+    what = (f"{precision} plan {latents_per_workgroup}/{column_parts}/{num_splits} "
+            f"(N_latent={N_latent} N_input={N_input})")
+    if precision == "fp32":
+        if not HAS_OPTIMIZED_PLAN:
+            raise RuntimeError("this kernels.so does not export launch_optimized_plan_kernel")
+        inputs = tuple(_prep(a, batch_size) for a in (Q, K, V))
+
+        def one(bufs, out, _):
+            lib.launch_optimized_plan_kernel(bufs[0].f32, bufs[1].f32, bufs[2].f32, out.f32,
+                                             batch_size, N_latent, N_input, D,
+                                             latents_per_workgroup, num_splits, _NULL_STREAM)
+    elif precision in ("fp16", "bf16"):
+        if not HAS_WMMA_PLAN:
+            raise RuntimeError("this kernels.so does not export launch_wmma_plan_kernel")
+        bf16 = precision == "bf16"
+        inputs = _half_inputs(Q, K, V, batch_size, D, bf16)
+
+        def one(bufs, out, _):
+            lib.launch_wmma_plan_kernel(int(bf16), bufs[0].ptr, bufs[1].ptr, bufs[2].ptr,
+                                        out.f32, batch_size, N_latent, N_input, D,
+                                        latents_per_workgroup, column_parts, num_splits,
+                                        _NULL_STREAM)
+    else:
+        raise ValueError(f"precision {precision!r} is not fp32, fp16 or bf16")
+    out, mean_ms, std_ms, _ = _resident_run(one, inputs, (batch_size, N_latent, D), warmup,
+                                            iters, what)
+    return out, mean_ms, std_ms
+
+
 def wmma_splitk_partials(Q, K, V, batch_size, N_latent, N_input, D, num_splits, bf16=False):
     """Run the 16-bit split-K once; return (output, (po, pm, pl))."""
     fn = lib.launch_wmma_splitk_bf16_kernel if bf16 else lib.launch_wmma_splitk_kernel

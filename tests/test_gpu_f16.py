@@ -7,7 +7,6 @@ kernel's own error (P rounded to 16 bits, fp32 accumulation):
 rel <= 4e-3 for bf16 and <= 1e-3 for fp16.
 """
 
-import ctypes
 import math
 
 import numpy as np
@@ -83,18 +82,9 @@ def test_bitwise_repeatable(cw, oracle, bf16, b, nl, ni, s):
 def _run_plan(cw, q, k, v, bf16, lpw, cp, s):
     """One launch_wmma_plan_kernel call with the given plan; the output."""
     b, nl, d = q.shape
-    ni = k.shape[1]
-    bufs = [cw.DeviceBuffer.holding(a) for a in cw._half_inputs(q, k, v, b, d, bf16)]
-    out = cw.DeviceBuffer(b * nl * d * 4).zero()
-    try:
-        cw.lib.launch_wmma_plan_kernel(int(bf16), *[p.ptr for p in bufs], out.f32, b, nl, ni, d,
-                                       lpw, cp, s, ctypes.c_void_p(0))
-        cw._lib_error_check("launch_wmma_plan_kernel")
-        assert cw.cudart.cudaDeviceSynchronize() == 0
-        return out.download((b, nl, d))
-    finally:
-        for p in bufs + [out]:
-            p.close()
+    out, _, _ = cw.benchmark_plan_events(q, k, v, b, nl, k.shape[1], d, lpw, s, cp,
+                                         "bf16" if bf16 else "fp16", warmup=0, iters=1)
+    return out
 
 
 @pytest.mark.parametrize("bf16", [False, True], ids=["fp16", "bf16"])

@@ -6,8 +6,6 @@ experiments/bench_perceiver_ni.py:147-148).  Every case calls the HIP library
 through its C ABI (cuda_wrappers -> kernels.so).
 """
 
-import ctypes
-
 import numpy as np
 import pytest
 
@@ -60,17 +58,7 @@ def test_every_plan_form(cw, oracle, lpw, s):
     shape (latents past the last full block, a partial last key tile)."""
     b, nl, ni = 2, 80, 200
     q, k, v = oracle.make_inputs(b, nl, ni, 768, seed=43)
-    bufs = [cw.DeviceBuffer.holding(a) for a in (q, k, v)]
-    out = cw.DeviceBuffer(b * nl * 768 * 4).zero()
-    try:
-        cw.lib.launch_optimized_plan_kernel(*[p.f32 for p in bufs], out.f32, b, nl, ni, 768, lpw,
-                                            s, ctypes.c_void_p(0))
-        cw._lib_error_check("launch_optimized_plan_kernel")
-        assert cw.cudart.cudaDeviceSynchronize() == 0
-        res = out.download((b, nl, 768))
-    finally:
-        for p in bufs + [out]:
-            p.close()
+    res, _, _ = cw.benchmark_plan_events(q, k, v, b, nl, ni, 768, lpw, s, warmup=0, iters=1)
     fp32_gate(res, oracle.attention_f64(q, k, v))
 
 

@@ -53,3 +53,31 @@ def test_16bit_plans(cw, oracle, b, nl, ni, s, bf16):
     assert np.all(np.isfinite(out)) and oracle.rel_err(out, ref) < 2e-2
     out, _ = cw.wmma_splitk_partials(q, k, v, b, nl, ni, 768, min(s, ni), bf16=bf16)
     assert np.all(np.isfinite(out)) and oracle.rel_err(out, ref) < 2e-2
+
+
+@pytest.mark.parametrize("i", range(8))
+def test_every_plan_form(cw, oracle, i):
+    """Every workgroup form of both paths (fp32: 64, 32, 16 latents; 16-bit:
+    64 latents in one or two column parts, 32 latents) under a random split
+    count from 1 to the number of key tiles -- counts that leave trailing
+    splits empty included -- through the plan-override entry points, at the
+    random shapes above."""
+    b, nl, ni, _ = SHAPES[i]
+    rng = np.random.RandomState(1000 + i)
+    q, k, v = oracle.make_inputs(b, nl, ni, 768, seed=b * 7919 + nl * 31 + ni + 2)
+    ref = oracle.attention_f64(q, k, v)
+    for lpw in (64, 32, 16):
+        s = int(rng.randint(1, -(-ni // 16) + 1))
+        out, _, _ = cw.benchmark_plan_events(q, k, v, b, nl, ni, 768, lpw, s, warmup=0,
+                                             iters=1)
+        fp32_gate(out, ref)
+    precision = "bf16" if i % 2 else "fp16"
+    qh, kh, vh = cw._half_inputs(q, k, v, b, 768, precision == "bf16")
+    f = oracle.bf16_bits_to_f32 if precision == "bf16" else (lambda a: a.astype(np.float32))
+    ref16 = oracle.attention_f64(f(qh).astype(np.float64) * math.sqrt(768), f(kh), f(vh))
+    for lpw, cp in ((64, 1), (64, 2), (32, 1)):
+        s = int(rng.randint(1, -(-ni // 32) + 1))
+        out, _, _ = cw.benchmark_plan_events(q, k, v, b, nl, ni, 768, lpw, s, cp, precision,
+                                             warmup=0, iters=1)
+        assert np.all(np.isfinite(out)), (lpw, cp, s)
+        assert oracle.rel_err(out, ref16) < 2e-2, (lpw, cp, s)
