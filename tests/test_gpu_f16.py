@@ -171,6 +171,28 @@ def test_growing_scores_force_restarts(cw, oracle, bf16):
 
 
 @pytest.mark.parametrize("bf16", [False, True], ids=["fp16", "bf16"])
+@pytest.mark.parametrize("lpw,cp", [(64, 1), (64, 2), (32, 1)], ids=["64", "64x2cols", "32"])
+def test_restarts_in_every_form(cw, oracle, bf16, lpw, cp):
+    """The growing-scores problem above (keys in rising order, so every
+    workgroup restarts its pass) through each workgroup form, unsplit and
+    in two splits, via launch_wmma_plan_kernel."""
+    rng = np.random.RandomState(8)
+    nl, ni = 40, 200
+    u = rng.randn(768)
+    u /= np.linalg.norm(u)
+    q = (u * np.sqrt(768.0) * (1.0 + 0.01 * rng.randn(nl, 1))
+         + 0.1 * rng.randn(nl, 768))[None].astype(np.float32)
+    k = (np.arange(ni)[:, None] * (12.0 / np.sqrt(768.0)) * u
+         + 0.05 * rng.randn(ni, 768))[None].astype(np.float32)
+    v = rng.randn(1, ni, 768).astype(np.float32)
+    ref = _rounded_ref(oracle, cw, q, k, v, bf16)
+    for s in (1, 2):
+        out = _run_plan(cw, q, k, v, bf16, lpw, cp, s)
+        tight = oracle.rel_err(out, ref)
+        assert np.all(np.isfinite(out)) and tight <= 2 * TIGHT[bf16], (s, tight)
+
+
+@pytest.mark.parametrize("bf16", [False, True], ids=["fp16", "bf16"])
 def test_wide_workgroups_split_and_restart(cw, oracle, bf16):
     """Split-K partials and pass restarts on 64-latent workgroups: 64 copies
     of an 80-latent, 400-key problem whose scores rise by ~0.62 per key in
