@@ -2,8 +2,9 @@
 launch_wmma_bf16_kernel keep split partials in a workspace per (device,
 stream); here a small and a larger split shape are launched alternately on
 two streams (and on the null stream), so each stream's workspace is grown
-while the other stream's launches are in flight.  Every output must match
-the float64 oracle as when run alone."""
+while the other stream's launches are in flight; and from four host threads
+at once, each on its own stream.  Every output must match the float64
+oracle as when run alone."""
 
 import ctypes
 
@@ -78,4 +79,81 @@ def test_split_launches_on_two_streams(cw, oracle, entry):
                 for p in ins + [out]:
                     p.close()
         for s in streams[:2]:
+            hip.hipStreamDestroy(s)
+
+
+def test_host_threads_on_their_own_streams(cw, oracle):
+    """Four host threads launch concurrently (ctypes releases the GIL during
+    the call), each on its own created stream, alternating the split shapes
+    above -- two threads through launch_optimized_kernel, two through
+    launch_wmma_bf16_kernel -- so workspaces are created and grown from
+    several threads at once.  Each thread reads its own error state; every
+    output must match the float64 oracle."""
+    import threading
+
+    hip = _hip(cw)
+    hip.hipStreamSynchronize.argtypes = [P]
+    hip.hipStreamSynchronize.restype = ctypes.c_int
+    entries = ["launch_optimized_kernel", "launch_optimized_kernel",
+               "launch_wmma_bf16_kernel", "launch_wmma_bf16_kernel"]
+    streams = [P() for _ in entries]
+    for s in streams:
+        assert hip.hipStreamCreate(ctypes.byref(s)) == 0
+    cases = []  # per thread: (shape, ins, args, out, ref) per shape
+    try:
+        for t, entry in enumerate(entries):
+            row = []
+            for j, (b, nl, ni) in enumerate(SHAPES):
+                q, k, v = oracle.make_inputs(b, nl, ni, 768, seed=300 + 10 * t + j)
+                if entry == "launch_optimized_kernel":
+                    ins = [cw.DeviceBuffer.holding(a) for a in (q, k, v)]
+                    args = [p.f32 for p in ins]
+                    ref = oracle.attention_f64(q, k, v)
+                else:
+                    host = cw._half_inputs(q, k, v, b, 768, bf16=True)
+                    ins = [cw.DeviceBuffer.holding(a) for a in host]
+                    args = [p.ptr for p in ins]
+                    f = oracle.bf16_bits_to_f32
+                    ref = oracle.attention_f64(
+                        f(host[0]).astype(np.float64) * np.sqrt(768), f(host[1]), f(host[2]))
+                out = cw.DeviceBuffer(b * nl * 768 * 4).zero()
+                row.append(((b, nl, ni), ins, args, out, ref))
+            cases.append(row)
+        failures = []
+
+        def work(t):
+            try:
+                fn = getattr(cw.lib, entries[t])
+                for rep in range(9):
+                    (b, nl, ni), _, args, out, _ = cases[t][(rep + t) % len(SHAPES)]
+                    fn(*args, out.f32, b, nl, ni, 768, streams[t])
+                code = cw.lib.xattn_get_last_error()
+                if code != 0:
+                    failures.append((t, code, cw.lib.xattn_get_last_error_string()))
+                if hip.hipStreamSynchronize(streams[t]) != 0:
+                    failures.append((t, "stream"))
+            except Exception as e:  # reported after the join
+                failures.append((t, repr(e)))
+
+        threads = [threading.Thread(target=work, args=(t,)) for t in range(len(entries))]
+        for th in threads:
+            th.start()
+        for th in threads:
+            th.join()
+        assert not failures, failures
+        assert cw.cudart.hipDeviceSynchronize() == 0
+        for t, row in enumerate(cases):
+            for (b, nl, ni), _, _, out, ref in row:
+                got = out.download((b, nl, 768))
+                if entries[t] == "launch_optimized_kernel":
+                    fp32_gate(got, ref)
+                else:
+                    assert oracle.rel_err(got, ref) < 4e-3, (t, b, nl, ni)
+    finally:
+        assert cw.cudart.hipDeviceSynchronize() == 0
+        for row in cases:
+            for _, ins, _, out, _ in row:
+                for p in ins + [out]:
+                    p.close()
+        for s in streams:
             hip.hipStreamDestroy(s)
