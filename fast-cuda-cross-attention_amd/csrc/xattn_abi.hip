@@ -27,7 +27,9 @@ void set_error(int code, const char* fmt, ...) {
     va_start(ap, fmt);
     vsnprintf(buf, sizeof(buf), fmt, ap);
     va_end(ap);
-    if (g_err == XATTN_OK) g_err = code;
+    // The message belongs to the error xattn_get_last_error() will return.
+    if (g_err != XATTN_OK) return;
+    g_err = code;
     snprintf(g_msg, sizeof(g_msg), "%s", buf);
 }
 

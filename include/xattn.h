@@ -178,7 +178,8 @@ enum {
 /* Returns the first error recorded on this host thread since the last call,
  * and clears it (like hipGetLastError). */
 int xattn_get_last_error(void);
-/* Message of the most recent recorded error ("" if none). */
+/* Message of the error xattn_get_last_error() returns (or last returned):
+ * the first one recorded since the code was last read; "" if none. */
 const char* xattn_get_last_error_string(void);
 
 /* Replaces the ordinal-based cudaDeviceGetAttribute query of

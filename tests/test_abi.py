@@ -302,3 +302,21 @@ def test_validation_refuses_before_launch(cw):
     # empty problems are a no-op, not an error
     code, _ = _call(cw, "launch_optimized_kernel", null, null, null, null, 0, 0, 0, 768, s0)
     assert code == 0
+
+
+def test_unread_errors_keep_the_first(cw):
+    """Two refusals with no read between them: the code and the message are
+    both the first one's, like hipGetLastError; once read, the next refusal
+    is recorded afresh."""
+    F = ctypes.POINTER(ctypes.c_float)
+    dummy = ctypes.cast(ctypes.c_void_p(0x1000), F)
+    s0 = ctypes.c_void_p(0)
+    cw.lib.launch_optimized_kernel(dummy, dummy, dummy, dummy, 1, 64, 784, 100, s0)
+    cw.lib.launch_optimized_kernel(dummy, dummy, dummy, dummy, -1, 64, 784, 768, s0)
+    code, msg = cw.lib.xattn_get_last_error(), cw.lib.xattn_get_last_error_string().decode()
+    assert code == 2 and "dim=100" in msg and "negative" not in msg, msg
+    # the message stays readable after the code was read
+    assert "dim=100" in cw.lib.xattn_get_last_error_string().decode()
+    code, msg = _call(cw, "launch_optimized_kernel", dummy, dummy, dummy, dummy, -1, 64, 784,
+                      768, s0)
+    assert code == 1 and "negative" in msg, msg
