@@ -116,13 +116,14 @@ CASES = {
 
 
 def time_launches(cw, launch, steps, warmup):
-    """warmup launches, then `steps` launches each bracketed by HIP events on
-    the launch stream (the null stream); returns (wall_s, per-launch ms)."""
+    """Exactly `warmup` untimed launches (the first one's error state checked),
+    then `steps` launches each bracketed by HIP events on the launch stream
+    (the null stream); returns (wall_s, per-launch ms)."""
     stream = ctypes.c_void_p(0)
-    launch()
-    cw._lib_error_check("launch")
-    for _ in range(warmup):
+    for i in range(warmup):
         launch()
+        if i == 0:
+            cw._lib_error_check("launch")
     if cw.cudart.cudaDeviceSynchronize() != 0:
         raise RuntimeError("warmup failed")
     evs = [(ctypes.c_void_p(), ctypes.c_void_p()) for _ in range(steps)]

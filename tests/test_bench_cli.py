@@ -123,3 +123,56 @@ def test_plan_option():
             bench.parse_plan(bad)
     with pytest.raises(ValueError, match="16-bit"):
         bench.run_case(None, "cfg1", 1, 1, plan=(64, 1, 1))
+
+
+def test_exactly_warmup_then_steps_launches():
+    """time_launches makes exactly `warmup` untimed launches and then `steps`
+    timed ones, each timed launch between its own pair of events; the error
+    state is read after the first launch and after the timed region."""
+    import ctypes
+
+    sys.path.insert(0, ROOT)
+    import bench
+
+    class Rt:
+        def __init__(self):
+            self.log = []
+
+        def cudaDeviceSynchronize(self):
+            self.log.append("sync")
+            return 0
+
+        def cudaEventCreate(self, p):
+            return 0
+
+        def cudaEventRecord(self, ev, stream):
+            self.log.append("event")
+            return 0
+
+        def cudaEventElapsedTime(self, out, a, b):
+            ctypes.cast(out, ctypes.POINTER(ctypes.c_float)).contents.value = 0.5
+            return 0
+
+        def cudaEventDestroy(self, ev):
+            return 0
+
+    class Cw:
+        def __init__(self):
+            self.cudart = Rt()
+            self.checks = 0
+
+        def _lib_error_check(self, what):
+            self.checks += 1
+            self.cudart.log.append("check")
+
+    for warmup, steps in ((5, 20), (0, 3), (1, 1)):
+        cw = Cw()
+        wall, per = bench.time_launches(
+            cw, lambda: cw.cudart.log.append("launch"), steps, warmup)
+        log = cw.cudart.log
+        assert log.count("launch") == warmup + steps and len(per) == steps
+        assert all(x == 0.5 for x in per)
+        timed = log[log.index("event"):]
+        assert timed.count("launch") == steps and timed.count("event") == 2 * steps
+        assert log[:log.index("event")].count("launch") == warmup
+        assert cw.checks == (2 if warmup else 1)
