@@ -1,0 +1,114 @@
+"""Offsets past 2**31 elements and 2**32 bytes.  The reference forms batch
+offsets in 32-bit int (kernel_vectorized.cu:38-40, kernel_splitk.cu:73-74),
+which wraps once B * N * 768 passes 2**31; here every tensor of one launch
+passes it: Q and O (B=3600, N_latent=800) and K and V (N_input=784), through
+launch_optimized_kernel (fp32) and launch_wmma_bf16_kernel.  The batch
+elements repeat a few distinct blocks (device-to-device copies of random
+blocks), chosen per tensor with different periods, so an offset that wrapped
+would read rows of another block, or straddle two, and fail the check against
+the float64 oracle on the first batch element, those around the 2**32-byte
+and 2**31-element marks, and the last."""
+
+import ctypes
+import math
+
+import numpy as np
+import pytest
+
+from conftest import fp32_gate
+
+pytestmark = pytest.mark.gpu
+
+B, NL, NI, D = 3600, 800, 784, 768
+NQ, NKV = 5, 7  # distinct Q blocks, distinct K/V blocks
+D2H, D2D = 2, 3  # hipMemcpyKind
+
+
+def _checked(b_elems):
+    """Batch elements to check: the first, those whose tensor start crosses
+    2**32 bytes (fp32) and 2**31 elements, and the last."""
+    bs = {0, B - 1}
+    for mark in (2 ** 30, 2 ** 31):  # fp32 2**32 bytes; 2**31 elements (bf16 2**32 bytes)
+        first = -(-mark // b_elems)
+        bs.update({first - 1, first})
+    return sorted(b for b in bs if 0 <= b < B)
+
+
+def _filled(cw, blocks, period, nbytes_each):
+    """A device buffer of B batch elements, element b a copy of
+    blocks[b % period] (host arrays of nbytes_each bytes each)."""
+    src = cw.DeviceBuffer.holding(np.ascontiguousarray(np.stack(blocks[:period])))
+    dst = cw.DeviceBuffer(B * nbytes_each)
+    try:
+        for b in range(B):
+            err = cw.cudart.hipMemcpy(ctypes.c_void_p(dst.ptr.value + b * nbytes_each),
+                                      ctypes.c_void_p(src.ptr.value + (b % period) * nbytes_each),
+                                      nbytes_each, D2D)
+            assert err == 0, f"device copy {b}: HIP error {err}"
+    except Exception:
+        dst.close()
+        raise
+    finally:
+        src.close()
+    return dst
+
+
+def _row_block(cw, out, b):
+    host = np.empty((NL, D), np.float32)
+    err = cw.cudart.hipMemcpy(host.ctypes.data_as(ctypes.c_void_p),
+                              ctypes.c_void_p(out.ptr.value + b * NL * D * 4), host.nbytes, D2H)
+    assert err == 0, f"copy back {b}: HIP error {err}"
+    return host
+
+
+@pytest.mark.parametrize("precision", ["fp32", "bf16"])
+def test_offsets_past_2_31_elements(cw, oracle, precision):
+    assert B * NL * D > 2 ** 31 and B * NI * D > 2 ** 31
+    rng = np.random.RandomState(31)
+    qs = [rng.randn(NL, D).astype(np.float32) for _ in range(NQ)]
+    ks = [rng.randn(NI, D).astype(np.float32) for _ in range(NKV)]
+    vs = [rng.randn(NI, D).astype(np.float32) for _ in range(NKV)]
+    if precision == "fp32":
+        hq, hk, hv, esize = qs, ks, vs, 4
+    else:
+        # the 16-bit paths' host side: Q pre-scaled by 1/sqrt(D), all rounded to bf16
+        # (the three tensors go through one call per block, padded with block 0)
+        hq = [cw._half_inputs(q[None], ks[0][None], vs[0][None], 1, D, True)[0][0] for q in qs]
+        hk = [cw._half_inputs(qs[0][None], k[None], vs[0][None], 1, D, True)[1][0] for k in ks]
+        hv = [cw._half_inputs(qs[0][None], ks[0][None], v[None], 1, D, True)[2][0] for v in vs]
+        esize = 2
+    bufs = []
+    try:
+        for blocks, period, rows in ((hq, NQ, NL), (hk, NKV, NI), (hv, NKV, NI)):
+            bufs.append(_filled(cw, blocks, period, rows * D * esize))
+        out = cw.DeviceBuffer(B * NL * D * 4).zero()
+        bufs.append(out)
+        q, k, v = bufs[:3]
+        if precision == "fp32":
+            cw.lib.launch_optimized_kernel(q.f32, k.f32, v.f32, out.f32, B, NL, NI, D, None)
+        else:
+            cw.lib.launch_wmma_bf16_kernel(q.ptr, k.ptr, v.ptr, out.f32, B, NL, NI, D, None)
+        cw._raise_launch_errors(f"{precision} launch")
+        assert cw.cudart.hipDeviceSynchronize() == 0
+        bad = []
+        for b in sorted(set(_checked(NL * D)) | set(_checked(NI * D))):
+            got = _row_block(cw, out, b)
+            iq, ik = b % NQ, b % NKV
+            if precision == "fp32":
+                ref = oracle.attention_f64(qs[iq][None], ks[ik][None], vs[ik][None])[0]
+                try:
+                    fp32_gate(got, ref)
+                except AssertionError as e:
+                    bad.append(f"b={b}: {e}")
+            else:
+                f = oracle.bf16_bits_to_f32
+                ref = oracle.attention_f64(
+                    f(hq[iq])[None].astype(np.float64) * math.sqrt(D), f(hk[ik])[None],
+                    f(hv[ik])[None])[0]
+                rel = oracle.rel_err(got, ref)
+                if not (np.all(np.isfinite(got)) and rel < 2e-2):
+                    bad.append(f"b={b}: rel={rel:.3e}")
+        assert not bad, "\n".join(bad)
+    finally:
+        for buf in bufs:
+            buf.close()
