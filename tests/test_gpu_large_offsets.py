@@ -112,3 +112,59 @@ def test_offsets_past_2_31_elements(cw, oracle, precision):
     finally:
         for buf in bufs:
             buf.close()
+
+
+@pytest.mark.parametrize("precision", ["fp32", "bf16"])
+def test_split_partials_past_2_31_elements(cw, oracle, precision):
+    """Caller-owned split partials of B * N_latent * num_splits * 768 > 2**31
+    elements (B=64, N_latent=1024, 64 splits of N_input=784: chunks of 13
+    keys for fp32, so 61 splits carry keys, and of 16 for bf16, so 49 do; the
+    rest are empty and write sentinels) through
+    launch_splitk_kernel and launch_wmma_splitk_bf16_kernel; the merged
+    output is checked against the float64 oracle on batch elements whose
+    partials lie before, across and past the 2**31-element mark."""
+    b, nl, ni, s = 64, 1024, 784, 64
+    assert b * nl * s * D > 2 ** 31
+    rng = np.random.RandomState(64)
+    q = rng.randn(b, nl, D).astype(np.float32)
+    k = rng.randn(b, ni, D).astype(np.float32)
+    v = rng.randn(b, ni, D).astype(np.float32)
+    host = (q, k, v) if precision == "fp32" else cw._half_inputs(q, k, v, b, D, True)
+    rows = b * nl
+    bufs = []
+    try:
+        bufs = [cw.DeviceBuffer.holding(a) for a in host]
+        out = cw.DeviceBuffer(rows * D * 4).zero()
+        po = cw.DeviceBuffer(rows * s * D * 4)
+        pm, pl = cw.DeviceBuffer(rows * s * 4), cw.DeviceBuffer(rows * s * 4)
+        bufs += [out, po, pm, pl]
+        if precision == "fp32":
+            cw.lib.launch_splitk_kernel(*[x.f32 for x in bufs[:3]], out.f32, po.f32, pm.f32,
+                                        pl.f32, b, nl, ni, D, s, None)
+        else:
+            cw.lib.launch_wmma_splitk_bf16_kernel(*[x.ptr for x in bufs[:3]], out.f32, po.f32,
+                                                  pm.f32, pl.f32, b, nl, ni, D, s, None)
+        cw._raise_launch_errors(f"{precision} split launch")
+        assert cw.cudart.hipDeviceSynchronize() == 0
+        mark = 2 ** 31 // (s * D * nl)  # the batch element whose partials cross 2**31
+        res = out.download((b, nl, D))
+        bad = []
+        for bi in sorted({0, mark - 1, mark, mark + 1, b - 1}):
+            if precision == "fp32":
+                ref = oracle.attention_f64(q[bi:bi + 1], k[bi:bi + 1], v[bi:bi + 1])
+                try:
+                    fp32_gate(res[bi:bi + 1], ref)
+                except AssertionError as e:
+                    bad.append(f"b={bi}: {e}")
+            else:
+                f = oracle.bf16_bits_to_f32
+                qh, kh, vh = host
+                ref = oracle.attention_f64(f(qh[bi:bi + 1]).astype(np.float64) * math.sqrt(D),
+                                           f(kh[bi:bi + 1]), f(vh[bi:bi + 1]))
+                rel = oracle.rel_err(res[bi:bi + 1], ref)
+                if not (np.all(np.isfinite(res[bi])) and rel < 2e-2):
+                    bad.append(f"b={bi}: rel={rel:.3e}")
+        assert not bad, "\n".join(bad)
+    finally:
+        for buf in bufs:
+            buf.close()
