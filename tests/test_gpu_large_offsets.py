@@ -2,7 +2,8 @@
 offsets in 32-bit int (kernel_vectorized.cu:38-40, kernel_splitk.cu:73-74),
 which wraps once B * N * 768 passes 2**31; here every tensor of one launch
 passes it: Q and O (B=3600, N_latent=800) and K and V (N_input=784), through
-launch_optimized_kernel (fp32) and launch_wmma_bf16_kernel.  The batch
+launch_optimized_kernel (fp32), launch_wmma_kernel (fp16) and
+launch_wmma_bf16_kernel.  The batch
 elements repeat a few distinct blocks (device-to-device copies of random
 blocks), chosen per tensor with different periods, so an offset that wrapped
 would read rows of another block, or straddle two, and fail the check against
@@ -28,7 +29,7 @@ def _checked(b_elems):
     """Batch elements to check: the first, those whose tensor start crosses
     2**32 bytes (fp32) and 2**31 elements, and the last."""
     bs = {0, B - 1}
-    for mark in (2 ** 30, 2 ** 31):  # fp32 2**32 bytes; 2**31 elements (bf16 2**32 bytes)
+    for mark in (2 ** 30, 2 ** 31):  # fp32 2**32 bytes; 2**31 elements (16-bit 2**32 bytes)
         first = -(-mark // b_elems)
         bs.update({first - 1, first})
     return sorted(b for b in bs if 0 <= b < B)
@@ -61,7 +62,12 @@ def _row_block(cw, out, b):
     return host
 
 
-@pytest.mark.parametrize("precision", ["fp32", "bf16"])
+def _widen(oracle, precision, a):
+    """16-bit host values as float32."""
+    return oracle.bf16_bits_to_f32(a) if precision == "bf16" else a.astype(np.float32)
+
+
+@pytest.mark.parametrize("precision", ["fp32", "fp16", "bf16"])
 def test_offsets_past_2_31_elements(cw, oracle, precision):
     assert B * NL * D > 2 ** 31 and B * NI * D > 2 ** 31
     rng = np.random.RandomState(31)
@@ -71,11 +77,12 @@ def test_offsets_past_2_31_elements(cw, oracle, precision):
     if precision == "fp32":
         hq, hk, hv, esize = qs, ks, vs, 4
     else:
-        # the 16-bit paths' host side: Q pre-scaled by 1/sqrt(D), all rounded to bf16
-        # (the three tensors go through one call per block, padded with block 0)
-        hq = [cw._half_inputs(q[None], ks[0][None], vs[0][None], 1, D, True)[0][0] for q in qs]
-        hk = [cw._half_inputs(qs[0][None], k[None], vs[0][None], 1, D, True)[1][0] for k in ks]
-        hv = [cw._half_inputs(qs[0][None], ks[0][None], v[None], 1, D, True)[2][0] for v in vs]
+        # the 16-bit paths' host side: Q pre-scaled by 1/sqrt(D), all rounded to
+        # fp16 / bf16 (one call per block, the other two tensors padded with block 0)
+        bf = precision == "bf16"
+        hq = [cw._half_inputs(q[None], ks[0][None], vs[0][None], 1, D, bf)[0][0] for q in qs]
+        hk = [cw._half_inputs(qs[0][None], k[None], vs[0][None], 1, D, bf)[1][0] for k in ks]
+        hv = [cw._half_inputs(qs[0][None], ks[0][None], v[None], 1, D, bf)[2][0] for v in vs]
         esize = 2
     bufs = []
     try:
@@ -87,7 +94,8 @@ def test_offsets_past_2_31_elements(cw, oracle, precision):
         if precision == "fp32":
             cw.lib.launch_optimized_kernel(q.f32, k.f32, v.f32, out.f32, B, NL, NI, D, None)
         else:
-            cw.lib.launch_wmma_bf16_kernel(q.ptr, k.ptr, v.ptr, out.f32, B, NL, NI, D, None)
+            fn = cw.lib.launch_wmma_bf16_kernel if precision == "bf16" else cw.lib.launch_wmma_kernel
+            fn(q.ptr, k.ptr, v.ptr, out.f32, B, NL, NI, D, None)
         cw._raise_launch_errors(f"{precision} launch")
         assert cw.cudart.hipDeviceSynchronize() == 0
         bad = []
@@ -101,10 +109,10 @@ def test_offsets_past_2_31_elements(cw, oracle, precision):
                 except AssertionError as e:
                     bad.append(f"b={b}: {e}")
             else:
-                f = oracle.bf16_bits_to_f32
                 ref = oracle.attention_f64(
-                    f(hq[iq])[None].astype(np.float64) * math.sqrt(D), f(hk[ik])[None],
-                    f(hv[ik])[None])[0]
+                    _widen(oracle, precision, hq[iq])[None].astype(np.float64) * math.sqrt(D),
+                    _widen(oracle, precision, hk[ik])[None],
+                    _widen(oracle, precision, hv[ik])[None])[0]
                 rel = oracle.rel_err(got, ref)
                 if not (np.all(np.isfinite(got)) and rel < 2e-2):
                     bad.append(f"b={b}: rel={rel:.3e}")
@@ -114,13 +122,13 @@ def test_offsets_past_2_31_elements(cw, oracle, precision):
             buf.close()
 
 
-@pytest.mark.parametrize("precision", ["fp32", "bf16"])
+@pytest.mark.parametrize("precision", ["fp32", "fp16", "bf16"])
 def test_split_partials_past_2_31_elements(cw, oracle, precision):
     """Caller-owned split partials of B * N_latent * num_splits * 768 > 2**31
     elements (B=64, N_latent=1024, 64 splits of N_input=784: chunks of 13
-    keys for fp32, so 61 splits carry keys, and of 16 for bf16, so 49 do; the
-    rest are empty and write sentinels) through
-    launch_splitk_kernel and launch_wmma_splitk_bf16_kernel; the merged
+    keys for fp32, so 61 splits carry keys, and of 16 for fp16 / bf16, so 49
+    do; the rest are empty and write sentinels) through launch_splitk_kernel,
+    launch_wmma_splitk_kernel and launch_wmma_splitk_bf16_kernel; the merged
     output is checked against the float64 oracle on batch elements whose
     partials lie before, across and past the 2**31-element mark."""
     b, nl, ni, s = 64, 1024, 784, 64
@@ -129,7 +137,8 @@ def test_split_partials_past_2_31_elements(cw, oracle, precision):
     q = rng.randn(b, nl, D).astype(np.float32)
     k = rng.randn(b, ni, D).astype(np.float32)
     v = rng.randn(b, ni, D).astype(np.float32)
-    host = (q, k, v) if precision == "fp32" else cw._half_inputs(q, k, v, b, D, True)
+    host = ((q, k, v) if precision == "fp32"
+            else cw._half_inputs(q, k, v, b, D, precision == "bf16"))
     rows = b * nl
     bufs = []
     try:
@@ -142,8 +151,9 @@ def test_split_partials_past_2_31_elements(cw, oracle, precision):
             cw.lib.launch_splitk_kernel(*[x.f32 for x in bufs[:3]], out.f32, po.f32, pm.f32,
                                         pl.f32, b, nl, ni, D, s, None)
         else:
-            cw.lib.launch_wmma_splitk_bf16_kernel(*[x.ptr for x in bufs[:3]], out.f32, po.f32,
-                                                  pm.f32, pl.f32, b, nl, ni, D, s, None)
+            fn = (cw.lib.launch_wmma_splitk_bf16_kernel if precision == "bf16"
+                  else cw.lib.launch_wmma_splitk_kernel)
+            fn(*[x.ptr for x in bufs[:3]], out.f32, po.f32, pm.f32, pl.f32, b, nl, ni, D, s, None)
         cw._raise_launch_errors(f"{precision} split launch")
         assert cw.cudart.hipDeviceSynchronize() == 0
         mark = 2 ** 31 // (s * D * nl)  # the batch element whose partials cross 2**31
@@ -157,10 +167,8 @@ def test_split_partials_past_2_31_elements(cw, oracle, precision):
                 except AssertionError as e:
                     bad.append(f"b={bi}: {e}")
             else:
-                f = oracle.bf16_bits_to_f32
-                qh, kh, vh = host
-                ref = oracle.attention_f64(f(qh[bi:bi + 1]).astype(np.float64) * math.sqrt(D),
-                                           f(kh[bi:bi + 1]), f(vh[bi:bi + 1]))
+                qh, kh, vh = (_widen(oracle, precision, a[bi:bi + 1]) for a in host)
+                ref = oracle.attention_f64(qh.astype(np.float64) * math.sqrt(D), kh, vh)
                 rel = oracle.rel_err(res[bi:bi + 1], ref)
                 if not (np.all(np.isfinite(res[bi])) and rel < 2e-2):
                     bad.append(f"b={bi}: rel={rel:.3e}")
