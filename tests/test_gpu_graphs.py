@@ -1,4 +1,6 @@
-"""Split launches of launch_optimized_kernel inside HIP stream capture.
+"""Split launches inside HIP stream capture: launch_optimized_kernel, and
+(last test) launch_wmma_bf16_kernel, launch_splitk_kernel with caller
+scratch and launch_optimized_kernel_noalloc in one graph.
 
 The shape B=1, N_latent=64, N_input=784 is planned with key splits, so the
 launch uses its stream's library workspace.  With the workspace already
@@ -172,3 +174,78 @@ def test_captured_split_launch_replays(cw, oracle):
         h.hipStreamDestroy(stream)
 
 
+
+
+def test_captured_16bit_scratch_and_noalloc_launches_replay(cw, oracle):
+    """One graph holding three split launches of B=1 N_latent=64
+    N_input=784: launch_wmma_bf16_kernel (its plan splits the keys, so it
+    uses the stream's workspace, sized by an eager launch first),
+    launch_splitk_kernel with caller-owned scratch (7 splits) and
+    launch_optimized_kernel_noalloc (static scratch).  Replayed four times,
+    outputs cleared before each replay (outside the graph) and eager launches
+    of the same entry points on the null stream between replays; every
+    replay must match the float64 oracle."""
+    import math
+
+    b, nl, ni, s = 1, 64, 784, 7
+    cu, _ = cw.device_info()
+    assert cw.wmma_plan(b, nl, ni, cu)[1] > 1 and cw.f32_plan(b, nl, ni, cu)[1] > 1
+    assert cw.HAS_NOALLOC
+    q, k, v = oracle.make_inputs(b, nl, ni, 768, seed=21)
+    ref32 = oracle.attention_f64(q, k, v)
+    hq, hk, hv = cw._half_inputs(q, k, v, b, 768, True)
+    f = oracle.bf16_bits_to_f32
+    ref16 = oracle.attention_f64(f(hq).astype(np.float64) * math.sqrt(768), f(hk), f(hv))
+    h = _hip(cw)
+    stream = P()
+    assert h.hipStreamCreate(ctypes.byref(stream)) == 0
+    bufs = []
+    graph, exe = P(), P()
+    try:
+        d32 = [cw.DeviceBuffer.holding(a) for a in (q, k, v)]
+        d16 = [cw.DeviceBuffer.holding(a) for a in (hq, hk, hv)]
+        o16, osk, ona = (cw.DeviceBuffer(b * nl * 768 * 4) for _ in range(3))
+        po = cw.DeviceBuffer(b * nl * s * 768 * 4)
+        pm, pl = cw.DeviceBuffer(b * nl * s * 4), cw.DeviceBuffer(b * nl * s * 4)
+        bufs = d32 + d16 + [o16, osk, ona, po, pm, pl]
+        outs = (o16, osk, ona)
+
+        def launches(st):
+            cw.lib.launch_wmma_bf16_kernel(*[x.ptr for x in d16], o16.f32, b, nl, ni, 768, st)
+            cw.lib.launch_splitk_kernel(*[x.f32 for x in d32], osk.f32, po.f32, pm.f32, pl.f32,
+                                        b, nl, ni, 768, s, st)
+            cw.lib.launch_optimized_kernel_noalloc(*[x.f32 for x in d32], ona.f32, b, nl, ni,
+                                                   768, st)
+
+        def check():
+            rel = oracle.rel_err(o16.download((b, nl, 768)), ref16)
+            assert rel < 2e-2, f"bf16 rel={rel:.3e}"
+            fp32_gate(osk.download((b, nl, 768)), ref32)
+            fp32_gate(ona.download((b, nl, 768)), ref32)
+
+        launches(stream)  # sizes this stream's workspace for the bf16 plan
+        cw._lib_error_check("eager launches")
+        assert h.hipStreamSynchronize(stream) == 0
+        check()
+        graph = _capture(h, stream, lambda: launches(stream))
+        cw._lib_error_check("captured launches")
+        assert h.hipGraphInstantiate(ctypes.byref(exe), graph, None, None, 0) == 0
+        for rep in range(4):
+            for o in outs:
+                o.zero()
+            assert h.hipGraphLaunch(exe, stream) == 0
+            assert h.hipStreamSynchronize(stream) == 0
+            check()
+            launches(P(0))  # eager work between replays
+            cw._lib_error_check("eager launches between replays")
+            assert cw.cudart.hipDeviceSynchronize() == 0
+            check()
+    finally:
+        assert cw.cudart.hipDeviceSynchronize() == 0
+        if exe:
+            h.hipGraphExecDestroy(exe)
+        if graph:
+            h.hipGraphDestroy(graph)
+        for x in bufs:
+            x.close()
+        h.hipStreamDestroy(stream)
