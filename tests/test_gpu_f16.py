@@ -222,3 +222,22 @@ def test_wide_workgroups_split_and_restart(cw, oracle, bf16):
     assert np.all(pm > -oracle.FLT_MAX) and np.all(pl > 0)
     pm = pm.reshape(b, nl, 2)
     assert np.array_equal(pm, np.broadcast_to(pm[:1], pm.shape))
+
+
+@pytest.mark.parametrize("bf16", [False, True], ids=["fp16", "bf16"])
+def test_nan_stays_where_the_reference_puts_it(cw, oracle, bf16):
+    """As the fp32 test of the same name: a NaN in one batch element's K
+    (whole output of that element NaN) or V (one column NaN), through the
+    16-bit planned launch (B=3 N_latent=64 N_input=100: a split plan); every
+    other value within the 16-bit gate."""
+    b, nl, ni = 3, 64, 100
+    for where in ("K", "V"):
+        q, k, v = oracle.make_inputs(b, nl, ni, 768, seed=78)
+        (k if where == "K" else v)[1, 37, 5] = np.nan
+        ref = oracle.attention_f64(q, k, v)
+        nan = np.isnan(ref)
+        assert nan[1].any() and not nan[[0, 2]].any()
+        out = _run(cw, q, k, v, bf16)
+        assert np.array_equal(np.isnan(out), nan), f"NaN in {where}: NaN pattern"
+        rel = oracle.rel_err(np.where(nan, 0.0, out), np.where(nan, 0.0, ref))
+        assert rel <= GATE, f"NaN in {where}: rel {rel:.3e}"

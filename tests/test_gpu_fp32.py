@@ -188,3 +188,23 @@ def test_legacy_drivers_2d_inputs(cw, oracle, fn):
     out = getattr(cw, fn)(q[0], k[0], v[0], 64, 784, 768)
     assert out.shape == (1, 64, 768)
     fp32_gate(out, oracle.attention_f64(q, k, v))
+
+
+def test_nan_stays_where_the_reference_puts_it(cw, oracle):
+    """A NaN in one batch element's K makes that element's whole output NaN
+    (every latent scores the key); a NaN in its V makes only that output
+    column NaN (each weight times it).  The reference's softmax formulation
+    (the oracle) puts them there; every other value must match it.  Through
+    the planned launch (B=3 N_latent=64 N_input=100: a split plan) and
+    launch_splitk_kernel with 3 splits."""
+    b, nl, ni = 3, 64, 100
+    for where in ("K", "V"):
+        q, k, v = oracle.make_inputs(b, nl, ni, 768, seed=77)
+        (k if where == "K" else v)[1, 37, 5] = np.nan
+        ref = oracle.attention_f64(q, k, v)
+        nan = np.isnan(ref)
+        assert nan[1].any() and not nan[[0, 2]].any()
+        for name, out in (("planned", _events(cw, "vectorized", q, k, v)),
+                          ("split-K", cw.splitk_partials(q, k, v, b, nl, ni, 768, 3)[0])):
+            assert np.array_equal(np.isnan(out), nan), f"NaN in {where}: {name} NaN pattern"
+            fp32_gate(np.where(nan, 0.0, out), np.where(nan, 0.0, ref))
