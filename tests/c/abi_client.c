@@ -1,9 +1,9 @@
 /*
  * A C program that uses kernels.so through include/xattn.h alone (no Python,
  * no torch): the fp32 entry point, split-K with caller-owned scratch, the
- * bf16 entry point and the two plan-override entry points on a small ragged
- * problem, each checked against a double-precision softmax(Q K^T / sqrt(D)) V
- * computed here.
+ * bf16 entry point, the two plan-override entry points and the no-allocation
+ * entry point on a small ragged problem, each checked against a
+ * double-precision softmax(Q K^T / sqrt(D)) V computed here.
  *
  *   gcc -std=c11 -D__HIP_PLATFORM_AMD__ -I/opt/rocm/include -Iinclude \
  *       tests/c/abi_client.c -L<dir of kernels.so> -l:kernels.so \
@@ -173,6 +173,12 @@ int main(void) {
     fails += status("launch_optimized_plan_kernel");
     HIP_OK(hipMemcpy(out, dout, nq * 4, hipMemcpyDeviceToHost));
     fails += check("launch_optimized_plan_kernel", out, ref, 1e-4, 1e-3);
+    /* the no-allocation twin of launch_optimized_kernel (static scratch) */
+    HIP_OK(hipMemset(dout, 0, nq * 4));
+    launch_optimized_kernel_noalloc(dq, dk, dv, dout, B, NL, NI, D, NULL);
+    fails += status("launch_optimized_kernel_noalloc");
+    HIP_OK(hipMemcpy(out, dout, nq * 4, hipMemcpyDeviceToHost));
+    fails += check("launch_optimized_kernel_noalloc", out, ref, 1e-4, 1e-3);
 
     /* an argument the kernels cannot run with is refused, not launched */
     launch_optimized_kernel(dq, dk, dv, dout, B, NL, NI, 64, NULL);
