@@ -151,6 +151,23 @@ __device__ inline void dma16_untracked(const void* sbase, unsigned voff, unsigne
         : "memory");
 }
 
+// The same DMA with M0 an input operand of the assembly: the compiler sets M0
+// itself (no save and restore around each load) and knows it changed.  OFF,
+// a constant byte offset below 4096, is the instruction's immediate: the
+// hardware adds it to every lane's source address and to the LDS
+// destination alike, so lds_byte is the destination minus OFF.  The one wait
+// state between the write of M0 and the load is the s_nop.
+template <int OFF>
+__device__ inline void dma16_m0(const void* sbase, unsigned voff, unsigned lds_byte) {
+    static_assert(OFF >= 0 && OFF < 4096, "global instruction offset range");
+    asm volatile(
+        "s_nop 0\n\t"
+        "global_load_lds_dwordx4 %0, %1 offset:%3"
+        :
+        : "v"(voff), "s"(sbase), "{m0}"(lds_byte), "i"(OFF)
+        : "memory");
+}
+
 // --------------------------------------------------------------------------
 // Phase clock: instrumented builds only (`make phaseclock` defines
 // XATTN_PHASE_CLOCK; the product build compiles none of it).  A kernel

@@ -163,24 +163,48 @@ void flash_f32_kernel(Params p) {
     // Phase ph (even: K of tile ph/2, odd: V of tile ph/2) -> buffer ph % 3.
     // Wavefront w's chunks cover tile rows r0 .. r0 + 3, three 1 KiB chunks
     // per row; chunk t of the phase is rows r0 + t / 3, floats 256 (t % 3)...
-    // Rows past k1 re-read row k1-1; their scores are masked to -inf and
-    // their weights are 0, so they only need to be finite.  The row is
-    // wave-uniform, so the clamp costs no vector instruction; the DMA is
-    // untracked (dma16_untracked), the phase waits below order it.
+    // Tile t's rows are the keys from win(t) on: k0 + 16 t, except that a
+    // partial last tile is shifted back to end at k1 (its first rows repeat
+    // keys of the tile before; the softmax masks them), and a range shorter
+    // than a tile keeps its window at k0 with the rows past the range
+    // re-reading its last row (masked too).  Every row read is a key of
+    // [k0, k1), and a chunk's source is one scalar base per phase and row
+    // plus the column offset as the instruction's immediate, with M0 set by
+    // the compiler: every scalar instruction costs issue time here (an fp32
+    // MFMA holds the SIMD while it runs).  The DMA is untracked; the phase
+    // waits below order it.
     const unsigned lds0 = lds_u32(lds);
     const int r0 = w * (CPW / ROW_CHUNKS);
     const unsigned lane16 = 16u * lane;
-    // K and V bases as scalar registers: the per-chunk offset is then scalar
-    // arithmetic, with no vector instruction between the MFMAs.
     const float* const Ks = uniform_ptr(Kb);
     const float* const Vs = uniform_ptr(Vb);
+    const int nk = k1 - k0;
+    // (The column-split forms, whose phases issue a chunk every one or two
+    // MFMA groups, keep the per-row clamp: their scalar registers would not
+    // hold a window base per row, and their phases are short.)
+    auto win = [&](int n0) {  // n0 = k0 + 16 t
+        return (DS == 1 && nk >= BN) ? min(n0, k1 - BN) : n0;
+    };
+    int roff[CPW / ROW_CHUNKS];  // byte offsets of this wavefront's rows in a window
+#pragma unroll
+    for (int r = 0; r < CPW / ROW_CHUNKS; ++r) roff[r] = min(r0 + r, min(nk, BN) - 1) * (kDim * 4);
     auto dma_chunk = [&](int ph, int t) {
         const int pr = ph < nphase ? ph : ph - 2;
         const int r = t / ROW_CHUNKS, c = t % ROW_CHUNKS;
-        const int key = min(k0 + (pr >> 1) * BN + r0 + r, k1 - 1);
-        const float* src = ((pr & 1) ? Vs : Ks) + ((size_t)key * kDim + c * (kWave * 4));
-        dma16_untracked(src, lane16,
-                        lds0 + 4u * (unsigned)((ph % NBUF) * BUF + (r0 + r) * ROW + c * (kWave * 4)));
+        // the row's first LDS byte; chunk c adds c KiB to it and to the source
+        const unsigned row_lds = lds0 + 4u * (unsigned)((ph % NBUF) * BUF + (r0 + r) * ROW);
+        if constexpr (DS == 1) {
+            const char* src = (const char*)((pr & 1) ? Vs : Ks) +
+                              ((size_t)win(k0 + (pr >> 1) * BN) * (kDim * 4) + roff[r]);
+            if (c == 0) dma16_m0<0>(src, lane16, row_lds);
+            else if (c == 1) dma16_m0<kWave * 16>(src, lane16, row_lds);
+            else dma16_m0<2 * kWave * 16>(src, lane16, row_lds);
+        } else {
+            const unsigned dst = row_lds + 4u * (unsigned)(c * (kWave * 4));
+            const int key = min(k0 + (pr >> 1) * BN + r0 + r, k1 - 1);
+            dma16_untracked(((pr & 1) ? Vs : Ks) + ((size_t)key * kDim + c * (kWave * 4)),
+                            lane16, dst);
+        }
     };
     auto issue = [&](int ph) {
 #pragma unroll
@@ -231,8 +255,14 @@ void flash_f32_kernel(Params p) {
 #pragma unroll
             for (int i = 0; i < 4; ++i) x[i] = s[i];
         } else {
+            // the window's keys are ws + 4g + i; those before n0 were scored
+            // by the tile before, those from k1 on are past the range
+            const int ws = win(n0);
 #pragma unroll
-            for (int i = 0; i < 4; ++i) x[i] = (n0 + 4 * g + i < k1) ? s[i] : -INFINITY;
+            for (int i = 0; i < 4; ++i) {
+                const int key = ws + 4 * g + i;
+                x[i] = (key >= n0 && key < k1) ? s[i] : -INFINITY;
+            }
         }
         const float tmax = fmaxf(fmaxf(x[0], x[1]), fmaxf(x[2], x[3]));
         if (!ref_set) {

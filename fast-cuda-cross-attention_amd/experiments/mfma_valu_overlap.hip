@@ -12,6 +12,8 @@
 //   2  fp32 MFMA waves + VALU waves  5  bf16 MFMA waves + VALU waves
 //   3  fp32 MFMA with the VALU work interleaved in the same waves
 //   6  bf16 MFMA with the VALU work interleaved in the same waves
+//   7  fp32 MFMA with 12 scalar-ALU instructions per iteration in the same
+//      waves (wave-uniform multiply-adds: what DMA address arithmetic issues)
 //
 // Prints, per mode, the launch time (HIP events) and the mean shader-clock
 // cycles (s_memtime) that the MFMA waves and the VALU waves take.  If the
@@ -60,7 +62,7 @@ __global__ __launch_bounds__(512) void probe(float* sink, unsigned long long* cy
     f4 c0 = {0.f, 0.f, 0.f, 0.f}, c1 = c0, c2 = c0, c3 = c0;
     float x0 = lane * 1e-3f, x1 = x0 + 0.1f, x2 = x0 + 0.2f, x3 = x0 + 0.3f;
     constexpr bool f32 = MODE == 0 || MODE == 2 || MODE == 3;
-    constexpr bool bf16 = MODE >= 4;
+    constexpr bool bf16 = MODE >= 4 && MODE <= 6;
     constexpr bool mixed = MODE == 3 || MODE == 6;
     constexpr bool valu_waves = MODE == 1 || MODE == 2 || MODE == 5;
     if (w < 4 && f32) {
@@ -91,8 +93,29 @@ __global__ __launch_bounds__(512) void probe(float* sink, unsigned long long* cy
     if (w >= 4 && valu_waves) {
         for (int i = 0; i < kIters; ++i) valu_step(x0, x1, x2, x3);
     }
+    unsigned su = __builtin_amdgcn_readfirstlane(blockIdx.x + 1u);
+    if (w < 4 && MODE == 7) {
+        // fp32 MFMAs with 12 scalar-ALU instructions per iteration (a
+        // shift-xor-multiply hash of a wave-uniform value, four times; written
+        // out so the compiler cannot fold it) between the second and third
+        for (int i = 0; i < kIters; ++i) {
+            c0 = __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, c0, 0, 0, 0);
+            c1 = __builtin_amdgcn_mfma_f32_16x16x4f32(b, a, c1, 0, 0, 0);
+            __builtin_amdgcn_sched_barrier(0);
+            unsigned tmp;
+#pragma unroll
+            for (int r = 0; r < 4; ++r)
+                asm volatile("s_lshr_b32 %1, %0, 7\n\ts_xor_b32 %0, %0, %1\n\t"
+                             "s_mul_i32 %0, %0, 0x9e3779b1"
+                             : "+s"(su), "=&s"(tmp));
+            __builtin_amdgcn_sched_barrier(0);
+            c2 = __builtin_amdgcn_mfma_f32_16x16x4f32(a, a, c2, 0, 0, 0);
+            c3 = __builtin_amdgcn_mfma_f32_16x16x4f32(b, b, c3, 0, 0, 0);
+        }
+    }
     const unsigned long long t1 = __builtin_amdgcn_s_memtime();
-    sink[blockIdx.x * 512 + threadIdx.x] = c0[0] + c1[1] + c2[2] + c3[3] + x0 + x1 + x2 + x3;
+    sink[blockIdx.x * 512 + threadIdx.x] =
+        c0[0] + c1[1] + c2[2] + c3[3] + x0 + x1 + x2 + x3 + (float)(su & 0xff);
     if (lane == 0) cycles[blockIdx.x * kWaves + w] = t1 - t0;
 }
 
@@ -101,15 +124,16 @@ typedef void (*Kernel)(float*, unsigned long long*);
 }  // namespace
 
 int main() {
-    const Kernel kernels[7] = {probe<0>, probe<1>, probe<2>, probe<3>,
-                               probe<4>, probe<5>, probe<6>};
-    const char* names[7] = {"fp32 MFMA waves only",
+    const Kernel kernels[8] = {probe<0>, probe<1>, probe<2>, probe<3>,
+                               probe<4>, probe<5>, probe<6>, probe<7>};
+    const char* names[8] = {"fp32 MFMA waves only",
                             "VALU waves only",
                             "fp32 MFMA waves + VALU waves",
                             "fp32 MFMA + VALU in the same waves",
                             "bf16 MFMA waves only",
                             "bf16 MFMA waves + VALU waves",
-                            "bf16 MFMA + VALU in the same waves"};
+                            "bf16 MFMA + VALU in the same waves",
+                            "fp32 MFMA + SALU in the same waves"};
     float* sink;
     unsigned long long* cyc;
     check(hipMalloc(&sink, sizeof(float) * kGroups * 512), "hipMalloc");
@@ -120,7 +144,7 @@ int main() {
     check(hipEventCreate(&e1), "hipEventCreate");
     printf("%-36s %10s %14s %14s\n", "mode", "us", "MFMA waves", "VALU waves");
     for (int rep = 0; rep < 2; ++rep) {
-        for (int m = 0; m < 7; ++m) {
+        for (int m = 0; m < 8; ++m) {
             hipLaunchKernelGGL(kernels[m], dim3(kGroups), dim3(512), 0, 0, sink, cyc);
             check(hipEventRecord(e0, 0), "hipEventRecord");
             hipLaunchKernelGGL(kernels[m], dim3(kGroups), dim3(512), 0, 0, sink, cyc);
