@@ -98,6 +98,7 @@ __global__ __launch_bounds__(512) void probe(float* sink, unsigned long long* cy
         // fp32 MFMAs with 12 scalar-ALU instructions per iteration (a
         // shift-xor-multiply hash of a wave-uniform value, four times; written
         // out so the compiler cannot fold it) between the second and third
+        // MFMA.
         for (int i = 0; i < kIters; ++i) {
             c0 = __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, c0, 0, 0, 0);
             c1 = __builtin_amdgcn_mfma_f32_16x16x4f32(b, a, c1, 0, 0, 0);
