@@ -366,8 +366,8 @@ constexpr H16Form kH16Forms[] = {{8, 1}, {8, 2}, {4, 1}};
 // Modelled time (µs) of one 16-bit launch of form f with S key splits of ct
 // 32-key tiles each, fitted (least squares on relative error) to 582 timed
 // bf16 launches on MI355X: every form and split count the planner weighs at
-// 27 shapes, B = 1..32, N_latent = 64..1024, N_input = 784..50176
-// (experiments/plan_campaign.py, experiments/fit_plan_cost.py).  Per
+// 27 shapes, B = 1..32, N_latent = 64..1024, N_input = 784..50176,
+// each timed through launch_wmma_plan_kernel.  Per
 // launch 3.22 µs; per round of workgroups, a 32-key tile costs 1.67 µs at 64
 // latents, 1.08 µs at 64 latents and half the columns, 1.22 µs at 32
 // latents, and 0.22 / 0.34 / 0.19 µs more when an unsplit launch fills every

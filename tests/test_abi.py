@@ -108,7 +108,8 @@ def test_f32_plan(cw):
 def test_wmma_plan(cw):
     # (latents per workgroup, column parts, key splits) of launch_wmma_kernel
     # on 256 CUs.  Where marked, the plan is the fastest of every form and
-    # split count timed at that shape on an MI355X (plan_campaign.py);
+    # split count timed at that shape on an MI355X (through
+    # launch_wmma_plan_kernel);
     # the others are within the spread of repeated timings of one plan.
     form = cw.wmma_plan_form
     assert form(32, 1024, 784, 256) == (64, 1, 1)   # measured best
