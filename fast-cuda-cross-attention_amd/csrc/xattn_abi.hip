@@ -7,6 +7,7 @@
 #include <string.h>
 
 #include <algorithm>
+#include <atomic>
 #include <mutex>
 #include <vector>
 
@@ -83,25 +84,43 @@ int device_cu_count() {
 // launch_wmma_kernel / launch_wmma_bf16_kernel: one block per (device,
 // stream), so split launches on different streams never share memory and
 // need no cross-stream ordering; on one stream, stream order serialises
-// them.  A block is allocated (hipMalloc) on a stream's first split launch
-// and replaced by a larger one, at least twice the size, when a launch needs
-// more.  A replaced block is never freed: launches already enqueued, or
-// kernels recorded into a graph, may still use it (its memory comes back at
-// process exit); geometric growth bounds the retired blocks' total by the
-// live block's size.  No launcher synchronises.  Under stream capture a
-// launch whose stream has a large enough block proceeds (the graph keeps
-// using that block, which is never freed); one that would have to allocate
-// is refused with XATTN_ERR_CAPTURE before anything is enqueued.
+// them.  hipStreamPerThread names a different stream in every host thread,
+// so for that handle the calling thread is part of the key.  A block is
+// allocated (hipMalloc) on a stream's first split launch and replaced by a
+// larger one, at least twice the size, when a launch needs more.  A
+// replaced block is never freed: launches already enqueued, or kernels
+// recorded into a graph, may still use it (its memory comes back at process
+// exit); geometric growth bounds the retired blocks' total by the live
+// block's size.  No launcher synchronises.
+//
+// Graphs.  Under stream capture a launch whose stream has a large enough
+// block proceeds, and the block then belongs to the graph: the next launch
+// on that stream outside capture retires it and takes a fresh block, so a
+// replay of the graph (on any stream) never shares partials with later
+// eager launches on the capturing stream.  A capturing launch that would
+// have to allocate is refused with XATTN_ERR_CAPTURE before anything is
+// enqueued.  Two graphs captured on one stream with no eager split launch
+// between the captures share a block, so their replays must not overlap.
 // --------------------------------------------------------------------------
 struct StreamWorkspace {
     int dev;
     hipStream_t stream;
+    uint64_t thread;         // the owning thread for hipStreamPerThread, else 0
     void* ptr;
     size_t bytes;
+    bool captured;           // a graph recorded launches that use this block
 };
 static std::mutex g_ws_mu;
 static std::vector<StreamWorkspace> g_ws;  // a handful of (device, stream) entries
 static std::vector<void*> g_ws_retired;     // replaced blocks, kept to process exit
+
+// A number of the calling host thread, never reused within the process (a
+// finished thread's std::thread::id can be).
+static uint64_t thread_number() {
+    static std::atomic<uint64_t> next{1};
+    thread_local const uint64_t mine = next++;
+    return mine;
+}
 
 // Is `stream` recording a graph?  A query that fails counts as capturing
 // (the launcher then refuses rather than allocate blindly).
@@ -127,12 +146,21 @@ class WorkspaceLease {
             set_error(XATTN_ERR_ALLOC, "workspace: no current device");
             return nullptr;
         }
+        const uint64_t owner = stream == hipStreamPerThread ? thread_number() : 0;
+        const bool capturing = stream_capturing(stream);
         lk_.lock();
         StreamWorkspace* w = nullptr;
         for (StreamWorkspace& e : g_ws)
-            if (e.dev == dev && e.stream == stream) w = &e;
-        if (w && w->bytes >= bytes) return w->ptr;
-        if (stream_capturing(stream)) {
+            if (e.dev == dev && e.stream == stream && e.thread == owner) w = &e;
+        if (w && w->bytes >= bytes) {
+            if (capturing) {
+                w->captured = true;
+                return w->ptr;
+            }
+            if (!w->captured) return w->ptr;
+            // an eager launch after a capture used this block: the graph
+            // keeps it, this stream takes a fresh one of the same size
+        } else if (capturing) {
             set_error(XATTN_ERR_CAPTURE,
                       "workspace: this split launch needs %zu bytes of workspace on a stream "
                       "that is capturing a graph and has %zu; make one launch of this (or a "
@@ -142,7 +170,8 @@ class WorkspaceLease {
             return nullptr;
         }
         size_t want = bytes;
-        if (w && want < 2 * w->bytes) want = 2 * w->bytes;
+        if (w && want < w->bytes) want = w->bytes;
+        if (w && !w->captured && want < 2 * w->bytes) want = 2 * w->bytes;
         void* p = nullptr;
         if (hipMalloc(&p, want) != hipSuccess) {
             (void)hipGetLastError();
@@ -153,8 +182,9 @@ class WorkspaceLease {
             g_ws_retired.push_back(w->ptr);
             w->ptr = p;
             w->bytes = want;
+            w->captured = false;
         } else {
-            g_ws.push_back(StreamWorkspace{dev, stream, p, want});
+            g_ws.push_back(StreamWorkspace{dev, stream, owner, p, want, false});
         }
         return p;
     }
@@ -174,40 +204,58 @@ class WorkspaceLease {
 // library runs on holds its own copy from module load until the process
 // ends.  On the host, `scratch` names a host-side stand-in, not device
 // memory: the device address is looked up once per device with
-// hipGetSymbolAddress (that device current) and only that address is handed
-// to kernels.  Every call on a GPU shares its copy; calls that overlap on
-// one GPU (different streams, or a graph replay beside an eager call) race.
-// Each launch overwrites every partial it merges (an empty split writes its
-// sentinel), so nothing has to be cleared between calls.
+// hipGetSymbolAddress (that device current, in xattn_noalloc_prepare) and
+// only that address is handed to kernels.  Each launch overwrites every
+// partial it merges (an empty split writes its sentinel), so nothing has to
+// be cleared between calls.
+//
+// Every call on a GPU shares its copy.  Outside stream capture, split calls
+// are ordered on the device by a library event per GPU: each call's stream
+// waits for the event (hipStreamWaitEvent: no host wait, no allocation),
+// the call enqueues its two kernels, and the event is recorded after the
+// merge, all under one lock, so overlapping calls from other streams or
+// host threads run one after the other.  A call under capture neither waits
+// nor records (a captured graph cannot depend on work outside it): a graph
+// replay that overlaps another split call on the same GPU races with it.
 // --------------------------------------------------------------------------
 constexpr size_t kNoallocScratchBytes = (size_t)64 << 20;  // 64 MiB per device
 static __device__ __align__(256) unsigned char scratch[kNoallocScratchBytes];
 
-static std::mutex g_scratch_mu;
-static void* g_scratch_ptr[256];
+struct NoallocDevice {
+    std::mutex mu;             // held across (wait, launches, record)
+    void* ptr = nullptr;       // device address of this GPU's `scratch`
+    hipEvent_t done = nullptr;  // recorded after the last split call's merge
+    bool recorded = false;
+};
+static NoallocDevice g_noalloc[256];
 
-// Device address of this device's `scratch`; nullptr (error recorded) if the
-// lookup fails.
-static void* noalloc_scratch(const char* who) {
-    int dev = 0;
-    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 256) {
-        (void)hipGetLastError();
-        set_error(XATTN_ERR_LAUNCH, "%s: no current device", who);
-        return nullptr;
-    }
-    std::lock_guard<std::mutex> lk(g_scratch_mu);
-    if (!g_scratch_ptr[dev]) {
+// Resolve `scratch` and create the ordering event for device `dev` (the
+// caller holds g_noalloc[dev].mu and has made `dev` current).  0 on success.
+static int noalloc_setup(int dev, const char* who) {
+    NoallocDevice& d = g_noalloc[dev];
+    if (!d.ptr) {
         void* ptr = nullptr;
         const hipError_t e = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
         if (e != hipSuccess || !ptr) {
             (void)hipGetLastError();
             set_error(XATTN_ERR_LAUNCH, "%s: hipGetSymbolAddress(scratch) failed: %s", who,
                       hipGetErrorString(e));
-            return nullptr;
+            return (int)(e != hipSuccess ? e : hipErrorInvalidSymbol);
         }
-        g_scratch_ptr[dev] = ptr;
+        d.ptr = ptr;
     }
-    return g_scratch_ptr[dev];
+    if (!d.done) {
+        hipEvent_t ev = nullptr;
+        const hipError_t e = hipEventCreateWithFlags(&ev, hipEventDisableTiming);
+        if (e != hipSuccess) {
+            (void)hipGetLastError();
+            set_error(XATTN_ERR_LAUNCH, "%s: hipEventCreateWithFlags failed: %s", who,
+                      hipGetErrorString(e));
+            return (int)e;
+        }
+        d.done = ev;
+    }
+    return 0;
 }
 
 // --------------------------------------------------------------------------
@@ -550,6 +598,35 @@ void xattn_wmma_plan_ex(int batch_size, int N_latent, int N_input, int cu_count,
     if (num_splits) *num_splits = S;
 }
 
+int xattn_lse_combine_parts(int rows, int num_splits, int cu_count) {
+    return lse_combine_parts(rows, num_splits, cu_count < 1 ? 1 : cu_count);
+}
+
+void xattn_lse_combine(const float* po, const float* pm, const float* pl, float* output,
+                       int rows, int num_splits, int column_parts, hipStream_t stream) {
+    const char* who = "xattn_lse_combine";
+    if (rows < 0) {
+        set_error(XATTN_ERR_INVALID_VALUE, "%s: negative row count %d", who, rows);
+        return;
+    }
+    if (!validate_splits(who, po, pm, pl, 1, rows, num_splits)) return;
+    if (rows > 0 && !output) {
+        set_error(XATTN_ERR_INVALID_VALUE, "%s: NULL output", who);
+        return;
+    }
+    if (column_parts != 0 && column_parts != 1 && column_parts != 2 && column_parts != 4) {
+        set_error(XATTN_ERR_INVALID_VALUE, "%s: column_parts %d (0, 1, 2 or 4)", who,
+                  column_parts);
+        return;
+    }
+    if (!validate_aligned16(who, po, po, po, output, po)) return;
+    if ((long long)rows * num_splits > 0x7fffffffLL) {
+        set_error(XATTN_ERR_INVALID_VALUE, "%s: rows*num_splits too large", who);
+        return;
+    }
+    launch_lse_combine(po, pm, pl, output, rows, num_splits, stream, column_parts);
+}
+
 void launch_naive_kernel(const float* Q, const float* K, const float* V, float* output,
                          int batch_size, int N_latent, int N_input, int dim, hipStream_t stream) {
     const char* who = "launch_naive_kernel";
@@ -653,6 +730,21 @@ void launch_optimized_plan_kernel(const float* Q, const float* K, const float* V
                   N_input == 0 ? 1 : num_splits, stream);
 }
 
+int xattn_noalloc_prepare(int device) {
+    if (device < 0 || device >= 256) return (int)hipErrorInvalidDevice;
+    int prev = 0;
+    hipError_t e = hipGetDevice(&prev);
+    if (e != hipSuccess) return (int)e;
+    if ((e = hipSetDevice(device)) != hipSuccess) return (int)e;
+    int rc;
+    {
+        std::lock_guard<std::mutex> lk(g_noalloc[device].mu);
+        rc = noalloc_setup(device, "xattn_noalloc_prepare");
+    }
+    e = hipSetDevice(prev);
+    return rc != 0 ? rc : (int)e;
+}
+
 void launch_optimized_kernel_noalloc(const float* Q, const float* K, const float* V,
                                      float* output, int batch_size, int N_latent, int N_input,
                                      int dim, hipStream_t stream) {
@@ -681,16 +773,50 @@ void launch_optimized_kernel_noalloc(const float* Q, const float* K, const float
                   kNoallocScratchBytes);
         return;
     }
-    char* base = (char*)noalloc_scratch(who);
-    if (!base) return;
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 256) {
+        (void)hipGetLastError();
+        set_error(XATTN_ERR_LAUNCH, "%s: no current device", who);
+        return;
+    }
+    const bool capturing = stream_capturing(stream);
+    NoallocDevice& nd = g_noalloc[dev];
+    std::lock_guard<std::mutex> lk(nd.mu);
+    if (!nd.ptr || !nd.done) {
+        if (capturing) {
+            set_error(XATTN_ERR_CAPTURE,
+                      "%s: first split call on device %d inside a stream capture; call "
+                      "xattn_noalloc_prepare(%d) (or make one call) before capturing",
+                      who, dev, dev);
+            return;
+        }
+        if (noalloc_setup(dev, who) != 0) return;
+    }
+    if (!capturing && nd.recorded && hipStreamWaitEvent(stream, nd.done, 0) != hipSuccess) {
+        const hipError_t e = hipGetLastError();
+        set_error(XATTN_ERR_LAUNCH, "%s: hipStreamWaitEvent failed: %s", who,
+                  hipGetErrorString(e));
+        return;
+    }
+    char* base = (char*)nd.ptr;
     float* po = (float*)base;
     float* pm = (float*)(base + po_bytes);
     float* pl = (float*)(base + po_bytes + ml_bytes);
     const int tiles = (N_input + 15) / 16;
     const int chunk = ((tiles + S - 1) / S) * 16;
-    if (launch_flash_f32(ds, Q, K, V, nullptr, po, pm, pl, batch_size, N_latent, N_input, S,
-                         chunk, stream))
-        launch_lse_combine(po, pm, pl, output, (int)rows, S, stream);
+    if (!launch_flash_f32(ds, Q, K, V, nullptr, po, pm, pl, batch_size, N_latent, N_input, S,
+                          chunk, stream))
+        return;
+    if (!launch_lse_combine(po, pm, pl, output, (int)rows, S, stream)) return;
+    if (!capturing) {
+        if (hipEventRecord(nd.done, stream) != hipSuccess) {
+            const hipError_t e = hipGetLastError();
+            set_error(XATTN_ERR_LAUNCH, "%s: hipEventRecord failed: %s", who,
+                      hipGetErrorString(e));
+            return;
+        }
+        nd.recorded = true;
+    }
 }
 
 void launch_splitk_kernel(const float* Q, const float* K, const float* V, float* output,

@@ -439,28 +439,34 @@ void flash_f32_kernel(Params p) {
 #endif
 }
 
-// Log-sum-exp merge of split partials (kernel_splitk.cu:186-236).  One
-// workgroup per (batch, latent) row, in P groups of 192 threads: every wave
-// reduces M = max pm and L = sum exp(pm - M) pl over the splits
-// (lane-strided), and thread c of group p accumulates float4 column c over
-// splits p, p + P, ... with 8 partial rows in flight at a time; the P group
-// sums are added in group order through LDS.  The first 8 partial rows and
-// each lane's first pm / pl are requested before the reductions (the
-// partials do not depend on M), so a row with few splits waits for one
-// round of loads, not three.  P = 1 when there are rows enough to fill the
-// device twice (HBM-bound: S * 3 KiB of po per row); P = 4 for fewer rows,
-// where one group's loads in flight would set the time.
-constexpr int kCombineThreads = kDim / 4;  // 192 threads per group
+// Log-sum-exp merge of split partials (kernel_splitk.cu:186-236).  Each
+// (batch, latent) row is merged by C workgroups, each owning 768 / C of its
+// columns, in P groups of 192 / C threads: every wave reduces M = max pm and
+// L = sum exp(pm - M) pl over the splits (lane-strided), and thread c of
+// group p accumulates float4 column c over splits p, p + P, ... with 8
+// partial rows in flight at a time; the P group sums are added in group
+// order through LDS.  Neither C nor the thread count changes any column's
+// arithmetic or its order, so the output is bit-identical for every C.  The
+// first 8 partial rows and each lane's first pm / pl are requested before
+// the reductions (the partials do not depend on M), so a row with few
+// splits waits for one round of loads, not three.  P = 1 when there are rows
+// enough to fill the device twice (HBM-bound: S * 3 KiB of po per row); P = 4
+// for fewer rows, where one group's loads in flight would set the time, and
+// then C > 1 spreads the rows' loads over more compute units.
+constexpr int kCombineThreads = kDim / 4;  // float4 columns of a row (192)
 
-template <int P>
-__global__ __launch_bounds__(kCombineThreads * P)
+template <int P, int C>
+__global__ __launch_bounds__(kCombineThreads / C * P)
 void lse_combine_kernel(const float* __restrict__ po, const float* __restrict__ pm,
                         const float* __restrict__ pl, float* __restrict__ out, int S) {
-    __shared__ f4 part[P > 1 ? (P - 1) * kCombineThreads : 1];
-    const size_t row = blockIdx.x;
+    constexpr int G = kCombineThreads / C;  // threads (float4 columns) per group
+    static_assert(kCombineThreads % C == 0, "column parts");
+    __shared__ f4 part[P > 1 ? (P - 1) * G : 1];
+    const size_t row = blockIdx.x / C;
     const int lane = threadIdx.x & 63;
-    const int c = threadIdx.x % kCombineThreads;
-    const int grp = threadIdx.x / kCombineThreads;
+    const int cl = threadIdx.x % G;
+    const int c = (int)(blockIdx.x % C) * G + cl;  // float4 column of the row
+    const int grp = threadIdx.x / G;
     const float* pmr = pm + row * S;
     const float* plr = pl + row * S;
     const f4* src = (const f4*)(po + row * S * kDim) + c;
@@ -504,11 +510,11 @@ void lse_combine_kernel(const float* __restrict__ po, const float* __restrict__ 
         for (int u = 0; u < 8; ++u) acc += wgt[u] * v[u];
     }
     if constexpr (P > 1) {
-        if (grp > 0) part[(grp - 1) * kCombineThreads + c] = acc;
+        if (grp > 0) part[(grp - 1) * G + cl] = acc;
         __syncthreads();
         if (grp > 0) return;
 #pragma unroll
-        for (int q = 1; q < P; ++q) acc += part[(q - 1) * kCombineThreads + c];
+        for (int q = 1; q < P; ++q) acc += part[(q - 1) * G + cl];
     }
     ((f4*)(out + row * kDim))[c] = acc * (1.0f / (L + 1e-6f));
 }
@@ -569,15 +575,43 @@ bool launch_flash_f32(int ds, const float* Q, const float* K, const float* V, fl
     return check_launch("flash_f32");
 }
 
+// Column parts of the merge: the most (1, 2 or 4) that still leave at most
+// one workgroup per CU.  The merge's time is its launch and one round trip
+// of loads; more parts help only while they reach CUs that would otherwise
+// stay idle (measured on MI355X: 64 rows, 4 parts 4.04 against 4.16 µs;
+// 256 rows, 2 parts 6.13 against 5.85 µs).
+int lse_combine_parts(int rows, int S, int cu) {
+    if (rows <= 0 || S <= 1 || rows >= 2 * cu) return 1;
+    int c = 1;
+    while (c < 4 && (long long)rows * (2 * c) <= cu) c *= 2;
+    return c;
+}
+
 bool launch_lse_combine(const float* po, const float* pm, const float* pl, float* out,
-                        int rows, int S, hipStream_t stream) {
+                        int rows, int S, hipStream_t stream, int parts) {
     if (rows <= 0) return true;
-    if (rows < 2 * device_cu_count() && S > 1)
-        hipLaunchKernelGGL(f32::lse_combine_kernel<4>, dim3(rows), dim3(4 * f32::kCombineThreads),
-                           0, stream, po, pm, pl, out, S);
-    else
-        hipLaunchKernelGGL(f32::lse_combine_kernel<1>, dim3(rows), dim3(f32::kCombineThreads), 0,
+    const bool few = rows < 2 * device_cu_count() && S > 1;
+    if (parts <= 0) parts = few ? lse_combine_parts(rows, S, device_cu_count()) : 1;
+    if (!few) parts = 1;
+    const long long nblk = (long long)rows * parts;
+    if (nblk > 0x7fffffffLL) {
+        set_error(XATTN_ERR_INVALID_VALUE, "lse_combine: grid of %lld workgroups too large", nblk);
+        return false;
+    }
+    const dim3 grid((unsigned)nblk);
+    const int G = f32::kCombineThreads / parts;
+    if (!few)
+        hipLaunchKernelGGL((f32::lse_combine_kernel<1, 1>), grid, dim3(f32::kCombineThreads), 0,
                            stream, po, pm, pl, out, S);
+    else if (parts == 4)
+        hipLaunchKernelGGL((f32::lse_combine_kernel<4, 4>), grid, dim3(4 * G), 0, stream, po, pm,
+                           pl, out, S);
+    else if (parts == 2)
+        hipLaunchKernelGGL((f32::lse_combine_kernel<4, 2>), grid, dim3(4 * G), 0, stream, po, pm,
+                           pl, out, S);
+    else
+        hipLaunchKernelGGL((f32::lse_combine_kernel<4, 1>), grid, dim3(4 * G), 0, stream, po, pm,
+                           pl, out, S);
     return check_launch("lse_combine");
 }
 

@@ -23,8 +23,12 @@ int f32_row_blocks(int NL, int ds);
 bool launch_flash_f32(int ds, const float* Q, const float* K, const float* V, float* out, float* po,
                       float* pm, float* pl, int B, int NL, int NI, int S, int chunk,
                       hipStream_t stream);
+// The LSE merge of split partials into out; parts <= 0 takes
+// lse_combine_parts' column parts (1, 2 or 4 workgroups per row; any choice
+// gives bit-identical output).
+int lse_combine_parts(int rows, int S, int cu);
 bool launch_lse_combine(const float* po, const float* pm, const float* pl, float* out, int rows,
-                        int S, hipStream_t stream);
+                        int S, hipStream_t stream, int parts = 0);
 
 // fp16 / bf16 MFMA flash kernel; Q/K/V are 16-bit bit patterns, Q pre-scaled
 // by 1/sqrt(768).  Same po semantics as launch_flash_f32.  nw = 8: 64-latent

@@ -246,6 +246,15 @@ HAS_OPTIMIZED_PLAN = _bind_optional("launch_optimized_plan_kernel",
 # for callers that cannot allocate (additive, no reference counterpart).
 HAS_NOALLOC = _bind_optional("launch_optimized_kernel_noalloc", [_F, _F, _F, _F, _I, _I, _I, _I,
                                                                  _P])
+if HAS_NOALLOC:
+    lib.xattn_noalloc_prepare.argtypes = [_I]
+    lib.xattn_noalloc_prepare.restype = ctypes.c_int
+# The LSE merge pass on its own (po, pm, pl, output, rows, splits, column
+# parts, stream; additive: the second launch of launch_splitk_kernel).
+HAS_LSE_COMBINE = _bind_optional("xattn_lse_combine", [_F, _F, _F, _F, _I, _I, _I, _P])
+if HAS_LSE_COMBINE:
+    lib.xattn_lse_combine_parts.argtypes = [_I, _I, _I]
+    lib.xattn_lse_combine_parts.restype = ctypes.c_int
 
 
 class DesignLimited(RuntimeError):
@@ -625,6 +634,29 @@ def benchmark_splitk_events(Q, K, V, batch_size, N_latent, N_input, D,
     out, mean_ms, std_ms = _splitk_run(launch, inputs, batch_size, N_latent, N_input, D,
                                        num_splits, warmup, iters, "split-K")
     return out, mean_ms, std_ms, num_splits
+
+
+def lse_combine(po, pm, pl, column_parts=0):
+    """Merge host split partials on the GPU (xattn_lse_combine): po [rows, S,
+    768], pm and pl [rows, S] -> output [rows, 768] fp32.  column_parts 0
+    takes the library's choice; 1, 2 and 4 force that many workgroups per
+    row (the output is the same bit for bit)."""
+    if not HAS_LSE_COMBINE:
+        raise RuntimeError("this kernels.so does not export xattn_lse_combine")
+    po = np.ascontiguousarray(po, dtype=np.float32)
+    pm = np.ascontiguousarray(pm, dtype=np.float32)
+    pl = np.ascontiguousarray(pl, dtype=np.float32)
+    rows, S, D = po.shape
+    if D != 768 or pm.shape != (rows, S) or pl.shape != (rows, S):
+        raise ValueError(f"partials of shapes {po.shape}, {pm.shape}, {pl.shape}: expected "
+                         f"[rows, S, 768], [rows, S], [rows, S]")
+    with DeviceBuffer.holding(po) as dpo, DeviceBuffer.holding(pm) as dpm, \
+            DeviceBuffer.holding(pl) as dpl, DeviceBuffer(rows * D * 4) as out:
+        lib.xattn_lse_combine(dpo.f32, dpm.f32, dpl.f32, out.f32, rows, S, int(column_parts),
+                              _NULL_STREAM)
+        _raise_launch_errors("xattn_lse_combine")
+        _hip_check(cudart.hipDeviceSynchronize(), "xattn_lse_combine: waiting for the kernel")
+        return out.download((rows, D))
 
 
 def splitk_partials(Q, K, V, batch_size, N_latent, N_input, D, num_splits):

@@ -23,14 +23,21 @@
  * Allocation: every entry point works on caller-owned buffers, except that
  * launch_optimized_kernel, launch_wmma_kernel and launch_wmma_bf16_kernel,
  * when their plan splits the keys, keep the split partials in a
- * library-owned workspace, one per (device, stream).  It is allocated with
- * hipMalloc on the first such launch on a stream and replaced (hipMalloc of
- * at least twice the size; the old block is kept, never freed, until the
- * process exits) when a later launch on that stream needs more.  Launches
- * on different streams never share a workspace.  While `stream` is capturing
- * a graph, such a launch proceeds only if the stream's workspace is already
- * large enough; otherwise it is refused with XATTN_ERR_CAPTURE and nothing
- * is enqueued.  launch_splitk_kernel and its 16-bit twins never allocate.
+ * library-owned workspace, one per (device, stream; and host thread for
+ * hipStreamPerThread, which names a different stream in each thread).  It
+ * is allocated with hipMalloc on the first such launch on a stream and
+ * replaced (hipMalloc of at least twice the size; the old block is kept,
+ * never freed, until the process exits) when a later launch on that
+ * stream needs more.  Launches on different streams never share a
+ * workspace.  While `stream` is capturing a graph, such a launch proceeds
+ * only if the stream's workspace is already large enough (otherwise it is
+ * refused with XATTN_ERR_CAPTURE and nothing is enqueued), and the block
+ * then belongs to the graph: the next launch on that stream outside capture
+ * takes a fresh block, so replays of the graph, on any stream, never share
+ * partials with later eager launches.  Two graphs captured on one stream
+ * with no eager split launch on it between the captures share a block:
+ * their replays must not overlap.  launch_splitk_kernel and its 16-bit
+ * twins never allocate.
  */
 #ifndef XATTN_H
 #define XATTN_H
@@ -93,14 +100,27 @@ void launch_optimized_plan_kernel(const float* Q, const float* K, const float* V
  * serving loops, harnesses that forbid hipMalloc).  Same plan, kernels and
  * results, bit for bit; split partials go to a static scratch array of
  * 64 MiB per device instead of the stream's workspace, and the call never
- * allocates or frees.  A plan whose partials
+ * allocates or frees device memory.  A plan whose partials
  * (batch_size * N_latent * splits * (dim + 2) * 4 bytes, splits from
  * xattn_f32_plan) exceed 64 MiB is refused with XATTN_ERR_UNSUPPORTED.
- * All calls on one GPU share its scratch: calls that overlap on a GPU (other
- * streams, graph replays) race. */
+ * All calls on one GPU share its scratch.  Outside stream capture, calls
+ * whose plan splits the keys are ordered on the GPU by a library event
+ * (each call's stream waits for the previous split call's merge; no host
+ * wait), so calls from several streams or host threads do not race.  A
+ * call made under capture is not ordered against others: a replay of that
+ * graph must not overlap another split call on the same GPU.  The first
+ * split call on a device resolves the scratch address and creates the
+ * event (xattn_noalloc_prepare); made under capture it is refused with
+ * XATTN_ERR_CAPTURE instead. */
 void launch_optimized_kernel_noalloc(const float* Q, const float* K, const float* V,
                                      float* output, int batch_size, int N_latent,
                                      int N_input, int dim, hipStream_t stream);
+/* No counterpart in the reference, for the callers of
+ * launch_optimized_kernel_noalloc: resolve device `device`'s scratch
+ * address and create its ordering event now (idempotent), e.g. before
+ * capturing a graph that calls it.  Allocates no device memory.  Returns a
+ * hipError_t value (0 on success); the current device is left unchanged. */
+int xattn_noalloc_prepare(int device);
 
 /* ---- split-K (key-parallel) fp32 -------------------------------------- */
 
@@ -115,6 +135,23 @@ void launch_splitk_kernel(const float* Q, const float* K, const float* V,
                           float* output, float* po, float* pm, float* pl,
                           int batch_size, int N_latent, int N_input, int dim,
                           int num_splits, hipStream_t stream);
+
+/* No reference counterpart (the merge pass of launch_splitk_kernel on its
+ * own, kernel_splitk.cu:186-236): output[r, :] = sum_s exp(pm[r,s] - M)
+ * po[r,s,:] / (sum_s exp(pm[r,s] - M) pl[r,s] + 1e-6), M = max_s pm[r,s],
+ * for rows r < rows (a row is one (batch, latent) pair; the layouts of
+ * launch_splitk_kernel's scratch with batch_size * N_latent = rows), dim
+ * 768; splits with pm = -FLT_MAX are skipped.  column_parts: workgroups
+ * per row, 1, 2 or 4, or 0 for the library's choice
+ * (xattn_lse_combine_parts); every choice gives bit-identical output.
+ * Refused with XATTN_ERR_INVALID_VALUE for other values, num_splits < 1 or
+ * NULL pointers with rows > 0. */
+void xattn_lse_combine(const float* po, const float* pm, const float* pl,
+                       float* output, int rows, int num_splits,
+                       int column_parts, hipStream_t stream);
+/* Workgroups per row the merge uses for rows rows of num_splits splits on a
+ * device of cu_count compute units (no reference counterpart). */
+int xattn_lse_combine_parts(int rows, int num_splits, int cu_count);
 
 /* ---- fp16 / bf16 MFMA (fp32 accumulate, fp32 softmax, fp32 output) ----- */
 

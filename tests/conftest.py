@@ -41,3 +41,24 @@ def fp32_gate(out, ref, atol=1e-4, rtol=1e-3):
     assert np.all(np.isfinite(out)), "non-finite output"
     assert ma <= atol and rel <= rtol, f"max_abs={ma:.3e} rel={rel:.3e}"
     return ma, rel
+
+
+# 16-bit gates: rel <= 2e-2 against the fp32 oracle on the unrounded inputs
+# (the reduced-precision contract), and, against the oracle evaluated on the
+# rounded inputs the kernel sees, the kernel's own error bound TIGHT16 (P
+# rounded to 16 bits, fp32 accumulation), times a margin where the shapes
+# are many and ragged.
+GATE16 = 2e-2
+TIGHT16 = {False: 1e-3, True: 4e-3}
+
+
+def gate16(out, ref_unrounded, ref_rounded, bf16, margin=2.0):
+    """Both 16-bit gates; returns (rel vs unrounded, rel vs rounded)."""
+    import xattn_oracle as o
+    assert np.all(np.isfinite(out)), "non-finite output"
+    rel = o.rel_err(out, ref_unrounded)
+    tight = o.rel_err(out, ref_rounded)
+    assert rel <= GATE16, f"rel vs fp32 oracle {rel:.3e} > {GATE16}"
+    assert tight <= margin * TIGHT16[bf16], \
+        f"rel vs rounded-input oracle {tight:.3e} > {margin * TIGHT16[bf16]:.1e}"
+    return rel, tight

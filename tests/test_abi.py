@@ -321,3 +321,35 @@ def test_unread_errors_keep_the_first(cw):
     code, msg = _call(cw, "launch_optimized_kernel", dummy, dummy, dummy, dummy, -1, 64, 784,
                       768, s0)
     assert code == 1 and "negative" in msg, msg
+
+
+def test_merge_column_parts_choice(cw):
+    """Workgroups per row of the LSE merge: the most of 1, 2 or 4 that leave
+    at most one workgroup per CU (one for a single split)."""
+    parts = cw.lib.xattn_lse_combine_parts
+    assert parts(64, 25, 256) == 4     # configuration 1: 64 rows, 25 splits
+    assert parts(65, 8, 256) == 2
+    assert parts(128, 8, 256) == 2
+    assert parts(129, 8, 256) == 1
+    assert parts(256, 8, 256) == 1     # configuration 4: 256 rows
+    assert parts(512, 8, 256) == 1
+    assert parts(64, 1, 256) == 1
+    assert parts(0, 4, 256) == 1
+
+
+def test_merge_refuses_bad_arguments(cw):
+    """xattn_lse_combine refuses other column parts, num_splits < 1 and NULL
+    partials before any HIP call."""
+    F = ctypes.POINTER(ctypes.c_float)
+    dummy = ctypes.cast(ctypes.c_void_p(0x1000), F)
+    null = ctypes.cast(ctypes.c_void_p(0), F)
+    s0 = ctypes.c_void_p(0)
+    for parts in (3, 8, -1):
+        code, msg = _call(cw, "xattn_lse_combine", dummy, dummy, dummy, dummy, 64, 25, parts, s0)
+        assert code == 1 and "column_parts" in msg, msg
+    code, msg = _call(cw, "xattn_lse_combine", dummy, dummy, dummy, dummy, 64, 0, 0, s0)
+    assert code == 1 and "num_splits" in msg, msg
+    code, msg = _call(cw, "xattn_lse_combine", null, dummy, dummy, dummy, 64, 4, 0, s0)
+    assert code == 1 and "NULL" in msg, msg
+    code, msg = _call(cw, "xattn_lse_combine", dummy, dummy, dummy, dummy, -1, 4, 0, s0)
+    assert code == 1 and "negative" in msg, msg

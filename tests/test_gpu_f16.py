@@ -14,8 +14,7 @@ import pytest
 
 pytestmark = pytest.mark.gpu
 
-GATE = 2e-2
-TIGHT = {False: 1e-3, True: 4e-3}
+from conftest import GATE16 as GATE, TIGHT16 as TIGHT
 
 
 def _rounded_ref(oracle, cw, q, k, v, bf16):

@@ -157,6 +157,31 @@ def test_splitk_golden(cw, oracle):
     assert np.allclose(pm, g["pm"], atol=1e-5) and np.allclose(pl, g["pl"], rtol=1e-5)
 
 
+@pytest.mark.parametrize("b,nl,ni,q_std", [(1, 64, 784, 1.0), (1, 256, 4096, 0.02),
+                                           (2, 70, 300, 1.0), (1, 1000, 784, 1.0)])
+def test_merge_column_parts_bit_identical(cw, oracle, b, nl, ni, q_std):
+    """The LSE merge split over 2 or 4 workgroups per row (and the library's
+    choice) gives the one-workgroup-per-row merge's output bit for bit, on
+    the partials of configuration 1, of configuration 4 at N_input 4,096
+    (the library plan's split counts), of a ragged shape and of a shape with
+    rows enough for one workgroup per row; the split launch's own output
+    equals them."""
+    q, k, v = oracle.make_inputs(b, nl, ni, 768, seed=7, q_std=q_std)
+    cu, _ = cw.device_info()
+    s = cw.plan_num_splits(nl, ni, b, cu)
+    if s == 1:
+        s = 5
+    out, (po, pm, pl) = cw.splitk_partials(q, k, v, b, nl, ni, 768, s)
+    rows = b * nl
+    po, pm, pl = po.reshape(rows, s, 768), pm.reshape(rows, s), pl.reshape(rows, s)
+    merged = {c: cw.lse_combine(po, pm, pl, c) for c in (1, 2, 4, 0)}
+    for c in (2, 4, 0):
+        assert np.array_equal(merged[c], merged[1]), f"{c} column parts differ from 1"
+    assert np.array_equal(out.reshape(rows, 768), merged[1])
+    fp32_gate(out, oracle.attention_f64(q, k, v))
+    assert cw.lib.xattn_lse_combine_parts(rows, s, cu) in (1, 2, 4)
+
+
 @pytest.mark.parametrize("ni", [4096, 16384, 50176])
 def test_config4_long_input(cw, oracle, ni):
     cu, _ = cw.device_info()

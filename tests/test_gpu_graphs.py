@@ -176,6 +176,49 @@ def test_captured_split_launch_replays(cw, oracle):
 
 
 
+def test_graph_replayed_on_another_stream_beside_eager_launches(cw, oracle):
+    """A split launch captured on stream A owns A's workspace block from
+    then on: replays of the graph on stream B, each overlapping an eager
+    split launch of the same shape (other inputs) on A with no
+    synchronisation between the two, must both match the float64 oracle,
+    since the eager launches on A take a fresh block."""
+    cu, _ = cw.device_info()
+    assert cw.f32_plan(1, 64, 784, cu)[1] > 1
+    h = _hip(cw)
+    sa, sb = P(), P()
+    assert h.hipStreamCreate(ctypes.byref(sa)) == 0
+    assert h.hipStreamCreate(ctypes.byref(sb)) == 0
+    graphed = _Case(cw, oracle, 1, 64, 784, seed=41)
+    eager = _Case(cw, oracle, 1, 64, 784, seed=42)
+    graph, exe = P(), P()
+    try:
+        graphed.launch(cw, sa)  # sizes A's workspace
+        cw._lib_error_check("eager launch")
+        assert h.hipStreamSynchronize(sa) == 0
+        graph = _capture(h, sa, lambda: graphed.launch(cw, sa))
+        cw._lib_error_check("captured launch")
+        assert h.hipGraphInstantiate(ctypes.byref(exe), graph, None, None, 0) == 0
+        for rep in range(6):
+            graphed.out.zero()
+            eager.out.zero()
+            assert h.hipGraphLaunch(exe, sb) == 0
+            eager.launch(cw, sa)
+            cw._lib_error_check("eager launch beside a replay")
+            assert cw.cudart.hipDeviceSynchronize() == 0
+            graphed.check(cw)
+            eager.check(cw)
+    finally:
+        assert cw.cudart.hipDeviceSynchronize() == 0
+        if exe:
+            h.hipGraphExecDestroy(exe)
+        if graph:
+            h.hipGraphDestroy(graph)
+        graphed.close()
+        eager.close()
+        h.hipStreamDestroy(sa)
+        h.hipStreamDestroy(sb)
+
+
 def test_captured_16bit_scratch_and_noalloc_launches_replay(cw, oracle):
     """One graph holding three split launches of B=1 N_latent=64
     N_input=784: launch_wmma_bf16_kernel (its plan splits the keys, so it

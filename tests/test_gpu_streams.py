@@ -157,3 +157,75 @@ def test_host_threads_on_their_own_streams(cw, oracle):
                     p.close()
         for s in streams:
             hip.hipStreamDestroy(s)
+
+
+def test_host_threads_on_the_per_thread_stream(cw, oracle):
+    """Four host threads launch split shapes at once on hipStreamPerThread
+    (handle 2), which names a different stream in every thread: two threads
+    through launch_optimized_kernel, two through launch_wmma_bf16_kernel.
+    The library keys that handle's workspace by thread as well, so no two
+    threads share partials; every output must match the float64 oracle."""
+    import threading
+
+    hip = _hip(cw)
+    hip.hipStreamSynchronize.argtypes = [P]
+    hip.hipStreamSynchronize.restype = ctypes.c_int
+    per_thread = P(2)
+    entries = ["launch_optimized_kernel", "launch_optimized_kernel",
+               "launch_wmma_bf16_kernel", "launch_wmma_bf16_kernel"]
+    cases = []  # per thread, per repetition: (shape, ins, args, out, ref)
+    try:
+        for t, entry in enumerate(entries):
+            row = []
+            for rep in range(6):
+                b, nl, ni = SHAPES[(rep + t) % len(SHAPES)]
+                q, k, v = oracle.make_inputs(b, nl, ni, 768, seed=500 + 10 * t + rep)
+                if entry == "launch_optimized_kernel":
+                    ins = [cw.DeviceBuffer.holding(a) for a in (q, k, v)]
+                    args = [p.f32 for p in ins]
+                    ref = oracle.attention_f64(q, k, v)
+                else:
+                    host = cw._half_inputs(q, k, v, b, 768, bf16=True)
+                    ins = [cw.DeviceBuffer.holding(a) for a in host]
+                    args = [p.ptr for p in ins]
+                    f = oracle.bf16_bits_to_f32
+                    ref = oracle.attention_f64(
+                        f(host[0]).astype(np.float64) * np.sqrt(768), f(host[1]), f(host[2]))
+                out = cw.DeviceBuffer(b * nl * 768 * 4).zero()
+                row.append(((b, nl, ni), ins, args, out, ref))
+            cases.append(row)
+        failures = []
+
+        def work(t):
+            try:
+                fn = getattr(cw.lib, entries[t])
+                for (b, nl, ni), _, args, out, _ in cases[t]:
+                    fn(*args, out.f32, b, nl, ni, 768, per_thread)
+                code = cw.lib.xattn_get_last_error()
+                if code != 0:
+                    failures.append((t, code, cw.lib.xattn_get_last_error_string()))
+                if hip.hipStreamSynchronize(per_thread) != 0:
+                    failures.append((t, "per-thread stream"))
+            except Exception as e:  # reported after the join
+                failures.append((t, repr(e)))
+
+        threads = [threading.Thread(target=work, args=(t,)) for t in range(len(entries))]
+        for th in threads:
+            th.start()
+        for th in threads:
+            th.join()
+        assert not failures, failures
+        assert cw.cudart.hipDeviceSynchronize() == 0
+        for t, row in enumerate(cases):
+            for (b, nl, ni), _, _, out, ref in row:
+                got = out.download((b, nl, 768))
+                if entries[t] == "launch_optimized_kernel":
+                    fp32_gate(got, ref)
+                else:
+                    assert oracle.rel_err(got, ref) < 4e-3, (t, b, nl, ni)
+    finally:
+        assert cw.cudart.hipDeviceSynchronize() == 0
+        for row in cases:
+            for _, ins, _, out, _ in row:
+                for p in ins + [out]:
+                    p.close()
