@@ -154,6 +154,16 @@ __device__ inline lds_char* opaque_lds(unsigned byte_addr) {
     return (lds_char*)(uintptr_t)byte_addr;
 }
 
+// The lane index read again from the lane counter, opaque to the optimiser:
+// indices derived from threadIdx.x before the tile loop and used only after
+// it would otherwise stay live across the loop (and spill where the
+// registers are full).
+__device__ inline int fresh_lane_id() {
+    int v;
+    asm volatile("v_mbcnt_lo_u32_b32 %0, -1, 0\n\tv_mbcnt_hi_u32_b32 %0, -1, %0" : "=v"(v));
+    return v;
+}
+
 #ifdef XATTN_PHASE_CLOCK
 // lifetime stamps and per-tile sums of the last 16-bit launch: waits at the
 // two barriers, the score phase (with the softmax and the P write), the
@@ -166,7 +176,11 @@ __global__ __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(NW / 4,
 void flash16_kernel(Params p) {
     typedef typename Vec8<T>::type v8;
     typedef Shape<NW, CP> Sh;
-    constexpr int BM = Sh::BM, NCB = Sh::NCB, CPW = Sh::CPW, KPF = Sh::KPF, VPF = Sh::VPF;
+    constexpr int BM = Sh::BM, NCB = Sh::NCB, CPW = Sh::CPW, KPF = Sh::KPF;
+    // The split 64-latent form reads V one column block ahead: with two, its
+    // registers overflow and a Q fragment is reloaded from scratch every tile
+    // (a wait for all memory operations, the DMA included).
+    constexpr int VPF = PARTIAL && NW == 8 && CP == 1 ? 1 : Sh::VPF;
     constexpr int DW = Sh::DW, DB = Sh::DB, DWC = Sh::DWC, LROWV = Sh::LROWV;
     constexpr int CPWV = Sh::CPWV, CHUNKSV = Sh::CHUNKSV;
     __shared__ __attribute__((aligned(16))) char lds[NBUF * BUFB];
@@ -209,17 +223,20 @@ void flash16_kernel(Params p) {
     };
 
     if (k0 >= k1) {
-        // empty key range: sentinel partials (kernel_wmma_splitk.cu:65-76) or zeros
+        // empty key range: sentinel partials (kernel_wmma_splitk.cu:65-76) or
+        // zeros (the lane indices recomputed: this exit joins the main one)
+        const int lane_z = fresh_lane_id(), jz = lane_z & 15, gz = lane_z >> 4;
 #pragma unroll
         for (int cl = 0; cl < NCB; ++cl) {
-            const int q = q0 + QB * cl + j;
+            const int q = q0 + QB * cl + jz;
             if (q >= p.NL) continue;
-            float* dst = out_row(q) + d0 + 4 * g;
+            float* dst = out_row(q) + d0 + 4 * gz;
 #pragma unroll
             for (int e = 0; e < DB; ++e) *(f4*)(dst + 16 * e) = (f4){0.f, 0.f, 0.f, 0.f};
         }
-        if (PARTIAL && ch == 0 && kbo == 0 && g == 0 && qo < p.NL) {
-            const size_t pi = ((size_t)b * p.NL + qo) * p.S + split;
+        const int qz = q0 + QB * cbo + jz;
+        if (PARTIAL && ch == 0 && kbo == 0 && gz == 0 && qz < p.NL) {
+            const size_t pi = ((size_t)b * p.NL + qz) * p.S + split;
             p.pm[pi] = -FLT_MAX;
             p.pl[pi] = 0.f;
         }
@@ -280,8 +297,11 @@ void flash16_kernel(Params p) {
     auto dma_setup = [&](int ph) {
         const int pr = ph < nphase ? ph : ph - 2;
         const int tile = pr >> 1;
+        // the first row as a scalar, so the address stays in SGPRs (a
+        // per-lane copy would hold VGPRs across the tile loop)
+        const int row0 = __builtin_amdgcn_readfirstlane(tile * BN - row_lo(tile));
         Dma d;
-        d.src = uniform_ptr(((ph & 1) ? Vb : Kb) + (size_t)(tile * BN - row_lo(tile)) * ROWB);
+        d.src = uniform_ptr(((ph & 1) ? Vb : Kb) + (size_t)row0 * ROWB);
         d.m0 = lds0 + (unsigned)((ph % NBUF) * BUFB);
         return d;
     };
@@ -511,6 +531,8 @@ void flash16_kernel(Params p) {
     }
     XATTN_STAMP(clk_loop_end);
     wait_vmcnt<0>();  // the re-reads issued past the last phase
+    // lane (je, ge) as before the loop, recomputed rather than kept live
+    const int lane_e = fresh_lane_id(), je = lane_e & 15, ge = lane_e >> 4;
 
     // Combine the two key halves of each latent (max and sum, both against
     // the shared m_ref), then normalise (or, for a partial, rescale to the
@@ -519,19 +541,19 @@ void flash16_kernel(Params p) {
     // blocks' m_ref.
     m_true = wave_max16_groups(m_true);
     lsum = wave_sum16_groups(lsum);
-    if (g == 0) stats[w * QB + j] = make_float2(m_true, lsum);
-    if (g == 0 && kbo == 0) sref[cbo * QB + j] = m_ref;
+    if (ge == 0) stats[w * QB + je] = make_float2(m_true, lsum);
+    if (ge == 0 && kbo == 0) sref[cbo * QB + je] = m_ref;
     lds_barrier();
     float rsc[NCB];
 #pragma unroll
     for (int cb = 0; cb < NCB; ++cb) {
-        const float2 s0 = stats[(2 * cb) * QB + j], s1 = stats[(2 * cb + 1) * QB + j];
+        const float2 s0 = stats[(2 * cb) * QB + je], s1 = stats[(2 * cb + 1) * QB + je];
         const float mt = fmaxf(s0.x, s1.x);
-        const float factor = fast_exp2((sref[cb * QB + j] - mt) * kLog2e);
+        const float factor = fast_exp2((sref[cb * QB + je] - mt) * kLog2e);
         const float l = s0.y + s1.y;
         rsc[cb] = PARTIAL ? factor : factor / (l * factor + 1e-6f);
-        if (PARTIAL && ch == 0 && w == 0 && g == 0) {
-            const int q = q0 + QB * cb + j;
+        if (PARTIAL && ch == 0 && w == 0 && ge == 0) {
+            const int q = q0 + QB * cb + je;
             if (q < p.NL) {
                 const size_t pi = ((size_t)b * p.NL + q) * p.S + split;
                 p.pm[pi] = mt;  // scores are q.k with Q pre-scaled
@@ -551,11 +573,11 @@ void flash16_kernel(Params p) {
     for (int cl = 0; cl < NCB; ++cl) {
 #pragma unroll
         for (int t = 0; t < DB; ++t)
-            *(f4*)(stage + j * SROW + (16 * t + 4 * g) * 4) = acc[cl][t] * rsc[cl];
+            *(f4*)(stage + je * SROW + (16 * t + 4 * ge) * 4) = acc[cl][t] * rsc[cl];
         const int qb = q0 + QB * cl;
 #pragma unroll
         for (int k = 0; k < QB * DW / 4 / kWave; ++k) {
-            const int pc = k * kWave + lane;  // 16-byte piece of the slice
+            const int pc = k * kWave + lane_e;  // 16-byte piece of the slice
             const int r = pc / (DW / 4), c = pc % (DW / 4);
             const f4 o = *(const f4*)(stage + r * SROW + 16 * c);
             if (qb + r >= p.NL) continue;
