@@ -416,34 +416,23 @@ constexpr H16Form kH16Forms[] = {{8, 1}, {8, 2}, {4, 1}};
 // >= 0) to 1,164 timed launches on MI355X, bf16 and fp16: every form and
 // split count the planner weighs at 27 shapes, B = 1..32, N_latent =
 // 64..1024, N_input = 784..50176, each timed through launch_wmma_plan_kernel.
-// Per launch 5.04 µs; per round of workgroups 2.47 µs at 64 latents, 1.77 µs
-// at 64 latents and half the columns, 2.22 µs at 32 latents; per 32-key tile
-// and round 1.26 / 1.03 / 1.18 µs, growing with the fraction u of CUs the
-// launch keeps busy (+ 0.055 u + 0.083 u^2 / + 0.028 u + 0.123 u^2 /
-// + 0.040 u: the workgroups stream K and V from L2 at once) and, when an
-// unsplit launch fills every CU, by 0.40 / 0.16 / 0.08 µs more.  A split
-// launch adds the LSE merge, 5.57 µs + 0.30 µs per MB of partials written
-// and read back.  Its choice is the fastest timed plan for 39 of the 54
-// (type, shape) pairs and within 6.8 % of it for the others (0.62 % mean;
-// repeated timings of one plan spread by a few per cent).
+// Per launch 4.87 µs; per round of workgroups 1.26 µs, and per 32-key tile
+// and round 1.30 µs at 64 latents, 1.08 µs at 64 latents and half the
+// columns, 1.15 µs at 32 latents, plus 0.56 / 0.31 / 0.13 µs when an
+// unsplit launch fills every CU (its workgroups then all stream K and V from
+// L2 at once).  A split launch adds the LSE merge, 6.21 µs + 0.33 µs per MB
+// of partials written and read back.  Its choice is the fastest timed plan
+// for 40 of the 54 (type, shape) pairs and within 4.3 % of it for the others
+// (0.54 % mean), and the same in a later session the fit did not see (41 of
+// 54, 0.51 %); repeated timings of one plan spread by a few per cent.
 static double h16_cost(int B, int NL, int cu, H16Form f, long long S, long long ct) {
     const long long W = (long long)B * h16_row_blocks(NL, f.nw) * S * f.cp;
     const long long rounds = (W + cu - 1) / cu;
-    const double u = (double)std::min<long long>(W, cu) / cu;
     const bool full = S == 1 && W >= cu;
-    double round_us, tile_us;
-    if (f.nw == 4) {
-        round_us = 2.224;
-        tile_us = 1.183 + 0.040 * u + (full ? 0.084 : 0.0);
-    } else if (f.cp == 2) {
-        round_us = 1.765;
-        tile_us = 1.030 + (0.028 + 0.123 * u) * u + (full ? 0.163 : 0.0);
-    } else {
-        round_us = 2.469;
-        tile_us = 1.261 + (0.055 + 0.083 * u) * u + (full ? 0.403 : 0.0);
-    }
-    double t = 5.039 + (double)rounds * (round_us + (double)ct * tile_us);
-    if (S > 1) t += 5.572 + 0.295 * (double)B * NL * (double)S * (kDim * 4) * 1e-6;
+    double tile_us = f.nw == 4 ? 1.149 : f.cp == 2 ? 1.082 : 1.298;
+    if (full) tile_us += f.nw == 4 ? 0.128 : f.cp == 2 ? 0.311 : 0.556;
+    double t = 4.868 + (double)rounds * (1.263 + (double)ct * tile_us);
+    if (S > 1) t += 6.210 + 0.331 * (double)B * NL * (double)S * (kDim * 4) * 1e-6;
     return t;
 }
 

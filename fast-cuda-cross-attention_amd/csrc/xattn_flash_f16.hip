@@ -207,7 +207,6 @@ void flash16_kernel(Params p) {
     const int j = lane & 15, g = lane >> 4;
     const int q0 = rb * BM;                     // first latent of the workgroup
     const int cbo = w >> 1, kbo = w & 1;        // score unit: latent block, key half
-    const int qo = q0 + QB * cbo + j;           // ... and the latent of lane (j, *) in it
     const int d0 = ch * DWC + w * DW;           // output role: first column of the slice
 
     int k0 = 0, k1 = p.NI;
@@ -375,7 +374,7 @@ void flash16_kernel(Params p) {
     if (tid == 0) restart_flag = 0;
 
     const float tau_raw = tau_log2<T> / kLog2e;
-    // Softmax state of the owned unit, for latent qo: m_true: exact running
+    // Softmax state of the owned unit, for latent q0 + 16 cbo + j: m_true: exact running
     // max over this lane's keys of the half; m_ref: the reference of the
     // weights, the same for both halves of the latent and fixed for a pass;
     // lsum: the sum of this lane's weights.  The four lanes of a latent are

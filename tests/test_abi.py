@@ -111,18 +111,18 @@ def test_wmma_plan(cw):
     # an MI355X (through launch_wmma_plan_kernel, bf16 and fp16); repeated
     # timings of one plan spread by a few per cent.
     form = cw.wmma_plan_form
-    assert form(32, 1024, 784, 256) == (64, 1, 1)   # measured best
-    assert form(16, 512, 784, 256) == (32, 1, 1)    # fp16 best; bf16 ties (64, 2, 1)
-    assert form(8, 1024, 784, 256) == (32, 1, 1)    # fp16 best; bf16 0.3 % behind (64, 2, 1)
-    assert form(8, 512, 784, 256) == (64, 2, 1)     # measured best
-    assert form(4, 1024, 784, 256) == (64, 2, 1)    # measured best
-    assert form(16, 256, 784, 256) == (64, 2, 1)    # fp16 best; bf16 1.5 % behind (64, 1, 3)
-    assert form(16, 512, 1568, 256) == (64, 1, 2)   # measured best
+    assert form(32, 1024, 784, 256) == (64, 1, 1)    # measured best
+    assert form(16, 512, 784, 256) == (32, 1, 1)     # measured best
+    assert form(8, 1024, 784, 256) == (32, 1, 1)     # measured best
+    assert form(8, 512, 784, 256) == (64, 2, 1)      # measured best
+    assert form(4, 1024, 784, 256) == (64, 2, 1)     # measured best
     assert form(1, 1024, 16384, 256) == (64, 1, 16)  # measured best
-    assert form(1, 64, 784, 256) == (64, 2, 25)     # 1 % behind (64, 2, 13)
-    assert form(1, 256, 4096, 256) == (64, 2, 26)   # ties (64, 2, 22)
-    assert form(1, 256, 784, 256) == (64, 2, 13)    # 2-3 % behind (64, 2, 9)
-    assert form(2, 256, 50176, 256) == (64, 1, 32)  # 10 % ahead of the best timed, (64, 1, 25)
+    assert form(16, 256, 784, 256) == (64, 2, 1)     # fp16 best; bf16 2.7 % behind (64, 1, 3)
+    assert form(16, 512, 1568, 256) == (64, 1, 2)    # 1 % behind (32, 1, 1)
+    assert form(1, 64, 784, 256) == (64, 2, 25)      # 1 % behind (64, 2, 13)
+    assert form(1, 256, 4096, 256) == (64, 2, 26)    # within 1 % of (64, 2, 22)
+    assert form(1, 256, 784, 256) == (64, 2, 13)     # 3.5 % behind (64, 2, 7)
+    assert form(2, 256, 50176, 256) == (64, 1, 32)   # 9 % ahead of the best timed, (64, 1, 25)
     assert form(1, 64, 20, 256) == (64, 2, 1)       # one tile: nothing to split
     for b, nl, ni in [(32, 1024, 784), (1, 256, 4096), (1, 64, 20)]:
         assert cw.wmma_plan(b, nl, ni, 256) == (form(b, nl, ni, 256)[0], form(b, nl, ni, 256)[2])
