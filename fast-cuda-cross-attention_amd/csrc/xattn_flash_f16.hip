@@ -269,7 +269,8 @@ void flash16_kernel(Params p) {
     // tile is laid out the same way at its own row stride (LROWV: 50 pieces
     // and 25 chunks when the workgroup holds half of the columns).  The
     // per-lane source offsets are the same for every tile; the DMA is
-    // untracked (dma16_untracked): the phase waits order it.  Phases past the
+    // untracked inline assembly (dma16_m0: the compiler sets M0, with no save
+    // and restore around each chunk), ordered by the phase waits.  Phases past the
     // end re-read the last phase of the same kind into the buffer of phase
     // ph - 3, whose readers are done, so every tile issues the same way; the
     // DMA is drained after the loop.
@@ -306,18 +307,18 @@ void flash16_kernel(Params p) {
     };
     // chunk t (< CPW) of a K phase / (< CPWV) of a V phase
     auto dma_chunk_k = [&](const Dma& d, int t) {
-        dma16_untracked(d.src, doff[t], d.m0 + 1024 * (CPW * w + t));
+        dma16_m0<0>(d.src, doff[t], d.m0 + 1024 * (CPW * w + t));
     };
     auto dma_chunk_v = [&](const Dma& d, int t) {
-        if constexpr (CP == 1) dma16_untracked(d.src, doff[t], d.m0 + 1024 * (CPW * w + t));
-        else dma16_untracked(d.src, doffv[t], d.m0 + 1024 * (CPWV * w + t));
+        if constexpr (CP == 1) dma16_m0<0>(d.src, doff[t], d.m0 + 1024 * (CPW * w + t));
+        else dma16_m0<0>(d.src, doffv[t], d.m0 + 1024 * (CPWV * w + t));
     };
     auto dma_last_k = [&](const Dma& d) {
-        if (w == 0) dma16_untracked(d.src, doff[CPW], d.m0 + 1024 * (CHUNKS - 1));
+        if (w == 0) dma16_m0<0>(d.src, doff[CPW], d.m0 + 1024 * (CHUNKS - 1));
     };
     auto dma_last_v = [&](const Dma& d) {
         if constexpr (CP == 1) dma_last_k(d);
-        else if (w == 0) dma16_untracked(d.src, doffv[CPWV], d.m0 + 1024 * (CHUNKSV - 1));
+        else if (w == 0) dma16_m0<0>(d.src, doffv[CPWV], d.m0 + 1024 * (CHUNKSV - 1));
     };
     auto issue = [&](int ph) {
         const Dma d = dma_setup(ph);
