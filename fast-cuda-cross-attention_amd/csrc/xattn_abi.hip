@@ -333,23 +333,26 @@ int plan_splits(int B, int NL, int NI, int cu, int bm, int tile) {
 }
 
 // Modelled time (µs) of one fp32 launch with ds wavefronts per 16-latent
-// block (64/ds-latent workgroups) and S key splits of ct 16-key tiles each.
-// Fitted to launches on MI355X (256 CUs; 3 % mean error over B = 1..32,
-// N_latent = 64..1024, N_input = 784..50176): a 16-key tile costs a
-// workgroup 5.90 µs at 64 latents, 3.26 at 32 and 2.12 at 16 (smaller
-// workgroups stream more K/V from L2 and run the softmax more often per
-// FLOP), plus 0.39 µs per round of workgroups; a split launch adds the LSE
-// merge, 2.93 µs + 0.42 µs per MB of partials written and read back, + 0.07
-// µs per split while there are fewer merge rows (B * N_latent) than CUs.
+// block (64/ds-latent workgroups) and S key splits of ct 16-key tiles each,
+// fitted (least squares on relative error, coefficients >= 0) to 803 timed
+// launches on MI355X (every workgroup size and split count the planner weighs
+// at 31 shapes, B = 1..32, N_latent = 64..1024, N_input = 784..50176): a
+// 16-key tile costs a workgroup 5.62 µs at 64 latents, 2.99 at 32 and 1.72 at
+// 16 (smaller workgroups stream more K/V from L2 and run the softmax more
+// often per FLOP), plus 0.68 µs per round of workgroups; a split launch adds
+// the LSE merge, 10.67 µs + 0.36 µs per MB of partials written and read back,
+// + 0.08 µs per split while there are fewer merge rows (B * N_latent) than
+// CUs.  Its choice is the fastest timed plan at 27 of the 31 shapes, 0.48 %
+// slower on average and 4.4 % at worst.
 static double f32_cost(int B, int NL, int cu, int ds, long long S, long long ct) {
-    const double tile_us = ds == 1 ? 5.904 : ds == 2 ? 3.255 : 2.122;
+    const double tile_us = ds == 1 ? 5.620 : ds == 2 ? 2.986 : 1.716;
     const long long W = (long long)B * f32_row_blocks(NL, ds) * S;
     const long long rounds = (W + cu - 1) / cu;
-    double t = (double)rounds * ((double)ct * tile_us + 0.39);
+    double t = (double)rounds * (0.675 + (double)ct * tile_us);
     if (S > 1) {
         const double rows = (double)B * NL;
-        t += 2.927 + 0.424 * rows * (double)S * (kDim * 4) * 1e-6 +
-             0.07 * (double)S * std::max(0.0, 1.0 - rows / cu);
+        t += 10.668 + 0.355 * rows * (double)S * (kDim * 4) * 1e-6 +
+             0.08 * (double)S * std::max(0.0, 1.0 - rows / cu);
     }
     return t;
 }

@@ -81,6 +81,20 @@ struct Params {
     int B, NL, NI, S, chunk, row_blocks;
 };
 
+typedef __attribute__((address_space(3))) const float lds_cfloat;
+typedef __attribute__((address_space(3))) const f4 lds_cf4;
+
+// An LDS read base opaque to the optimiser (its float index within the tile
+// array): without it the compiler may re-associate (ring buffer + lane base
+// + fragment offset), hoist one register per fragment out of the tile loop
+// and add the buffer offset to each of them every phase, VALU work that an
+// fp32 MFMA stream cannot hide, instead of one base register plus immediates.
+__device__ inline lds_cfloat* opaque_lds_f(const float* lds, int index) {
+    unsigned a = lds_u32(lds) + 4u * (unsigned)index;
+    asm volatile("" : "+v"(a));
+    return (lds_cfloat*)(uintptr_t)a;
+}
+
 __device__ inline f4 mfma4(float a, float b, f4 c) {
     return __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, c, 0, 0, 0);
 }
@@ -179,11 +193,8 @@ void flash_f32_kernel(Params p) {
     const float* const Ks = uniform_ptr(Kb);
     const float* const Vs = uniform_ptr(Vb);
     const int nk = k1 - k0;
-    // (The column-split forms, whose phases issue a chunk every one or two
-    // MFMA groups, keep the per-row clamp: their scalar registers would not
-    // hold a window base per row, and their phases are short.)
     auto win = [&](int n0) {  // n0 = k0 + 16 t
-        return (DS == 1 && nk >= BN) ? min(n0, k1 - BN) : n0;
+        return nk >= BN ? min(n0, k1 - BN) : n0;
     };
     int roff[CPW / ROW_CHUNKS];  // byte offsets of this wavefront's rows in a window
 #pragma unroll
@@ -193,18 +204,11 @@ void flash_f32_kernel(Params p) {
         const int r = t / ROW_CHUNKS, c = t % ROW_CHUNKS;
         // the row's first LDS byte; chunk c adds c KiB to it and to the source
         const unsigned row_lds = lds0 + 4u * (unsigned)((ph % NBUF) * BUF + (r0 + r) * ROW);
-        if constexpr (DS == 1) {
-            const char* src = (const char*)((pr & 1) ? Vs : Ks) +
-                              ((size_t)win(k0 + (pr >> 1) * BN) * (kDim * 4) + roff[r]);
-            if (c == 0) dma16_m0<0>(src, lane16, row_lds);
-            else if (c == 1) dma16_m0<kWave * 16>(src, lane16, row_lds);
-            else dma16_m0<2 * kWave * 16>(src, lane16, row_lds);
-        } else {
-            const unsigned dst = row_lds + 4u * (unsigned)(c * (kWave * 4));
-            const int key = min(k0 + (pr >> 1) * BN + r0 + r, k1 - 1);
-            dma16_untracked(((pr & 1) ? Vs : Ks) + ((size_t)key * kDim + c * (kWave * 4)),
-                            lane16, dst);
-        }
+        const char* src = (const char*)((pr & 1) ? Vs : Ks) +
+                          ((size_t)win(k0 + (pr >> 1) * BN) * (kDim * 4) + roff[r]);
+        if (c == 0) dma16_m0<0>(src, lane16, row_lds);
+        else if (c == 1) dma16_m0<kWave * 16>(src, lane16, row_lds);
+        else dma16_m0<2 * kWave * 16>(src, lane16, row_lds);
     };
     auto issue = [&](int ph) {
 #pragma unroll
@@ -280,6 +284,14 @@ void flash_f32_kernel(Params p) {
         }
     };
 
+    // Per-lane LDS read bases of the tile loop.  The column-split forms take
+    // them opaque (their loops otherwise re-associate the fragment offsets
+    // as above); the 64-latent form's loop is compiled well without.
+    auto lds_base = [&](int index) -> lds_cfloat* {
+        if constexpr (DS == 1) return (lds_cfloat*)(lds + index);
+        else return opaque_lds_f(lds, index);
+    };
+
     XATTN_STAMP(clk_loop);
     XATTN_CLOCK_DECL(pc_wait = 0, pc_qk = 0, pc_pv = 0);
     for (bool first = true;; first = false) {  // passes over the keys; a second is rare
@@ -306,14 +318,14 @@ void flash_f32_kernel(Params p) {
             {
                 // K operand reads run two 4-MFMA groups ahead; the sched_barrier
                 // keeps the scheduler from hoisting all of them.
-                const float* kb = lds + (ph % NBUF) * BUF + j * ROW + 4 * g + 16 * NU * dp;
+                lds_cfloat* kb = lds_base((ph % NBUF) * BUF + j * ROW + 4 * g + 16 * NU * dp);
                 f4 s0 = {0.f, 0.f, 0.f, 0.f}, s1 = s0;
                 f4 kv[3];
-                kv[0] = *(const f4*)(kb);
-                kv[1] = *(const f4*)(kb + 16);
+                kv[0] = *(lds_cf4*)(kb);
+                kv[1] = *(lds_cf4*)(kb + 16);
 #pragma unroll
                 for (int u = 0; u < NU; ++u) {
-                    if (u + 2 < NU) kv[(u + 2) % 3] = *(const f4*)(kb + 16 * (u + 2));
+                    if (u + 2 < NU) kv[(u + 2) % 3] = *(lds_cf4*)(kb + 16 * (u + 2));
                     if (u % DSTEP == 0) dma_chunk(ph + 2, u / DSTEP);
                     const f4 k4 = kv[u % 3];
                     s0 = mfma4(k4[0], qr[u][0], s0);
@@ -351,15 +363,15 @@ void flash_f32_kernel(Params p) {
             {
                 // Group n = NT r + T: V[4g + r][64 (NT dp + T) + 4j .. +3] feeds
                 // the four MFMAs of output tiles (T, c = 0..3) for k-slab r.
-                const float* vb = lds + (ph % NBUF) * BUF + 4 * j + 4 * g * ROW + 64 * NT * dp;
+                lds_cfloat* vb = lds_base((ph % NBUF) * BUF + 4 * j + 4 * g * ROW + 64 * NT * dp);
                 f4 vv[3];
-                vv[0] = *(const f4*)(vb);
-                vv[1] = *(const f4*)(vb + (1 / NT) * ROW + 64 * (1 % NT));
+                vv[0] = *(lds_cf4*)(vb);
+                vv[1] = *(lds_cf4*)(vb + (1 / NT) * ROW + 64 * (1 % NT));
 #pragma unroll
                 for (int n = 0; n < 4 * NT; ++n) {
                     if (n + 2 < 4 * NT) {
                         const int rn = (n + 2) / NT, tn = (n + 2) % NT;
-                        vv[(n + 2) % 3] = *(const f4*)(vb + rn * ROW + 64 * tn);
+                        vv[(n + 2) % 3] = *(lds_cf4*)(vb + rn * ROW + 64 * tn);
                     }
                     if (n % DSTEP == 0) dma_chunk(ph + 2, n / DSTEP);
                     const int r = n / NT, T = n % NT;

@@ -83,17 +83,18 @@ def test_config3_batched_sweep(cw, oracle, b):
         fp32_gate(_events(cw, "vectorized", q, k, v), oracle.attention_f64(q, k, v))
 
 
-@pytest.mark.parametrize("b", [1, 100, 200])
-def test_growing_scores_force_rescales(cw, oracle, b):
+@pytest.mark.parametrize("lpw", [16, 32, 64])
+def test_growing_scores_force_rescales(cw, oracle, lpw):
     """Scores rise by ~12 per key across the key axis, so the running max grows
-    far past the lazy-rescale threshold many times within one row.  At this
-    shape launch_optimized_kernel splits the keys over workgroups, so the same
-    inputs also run through launch_splitk_kernel with one split: one workgroup
-    walks all 200 keys and must rescale on the way.  The batch (copies of one
-    element) sets the workgroup size: 16 latents at b=1, 32 at b=100, 64 at
-    b=200 on 256 compute units."""
+    far past the lazy-rescale threshold many times within one row.  Each
+    workgroup size (16, 32 or 64 latents) runs the keys unsplit through
+    launch_optimized_plan_kernel: one workgroup walks all 200 keys and must
+    rescale on the way.  The same inputs also run through the library's own
+    plan (launch_optimized_kernel, which splits the keys at this shape) and
+    launch_splitk_kernel with one split, whose partials must normalise to the
+    output."""
     rng = np.random.RandomState(8)
-    nl, ni = 40, 200
+    b, nl, ni = 2, 40, 200
     u = rng.randn(768)
     u /= np.linalg.norm(u)
     q = np.empty((1, nl, 768), np.float32)
@@ -107,12 +108,10 @@ def test_growing_scores_force_rescales(cw, oracle, b):
     order = np.argsort(k[0] @ u)
     k_sorted, v_sorted = k[:, order], v[:, order]
     q, k, v, k_sorted, v_sorted = (np.repeat(a, b, axis=0) for a in (q, k, v, k_sorted, v_sorted))
-    cu, _ = cw.device_info()
-    if cu == 256:
-        assert cw.lib.xattn_f32_split_latents(b, nl, ni, 1, cu) == {1: 16, 100: 32, 200: 64}[b]
-    fp32_gate(_events(cw, "vectorized", q, k, v), ref)
-    fp32_gate(_events(cw, "vectorized", q, k_sorted, v_sorted), ref)
     for kk, vv in ((k, v), (k_sorted, v_sorted)):
+        out, _, _ = cw.benchmark_plan_events(q, kk, vv, b, nl, ni, 768, lpw, 1, warmup=0, iters=1)
+        fp32_gate(out, ref)
+        fp32_gate(_events(cw, "vectorized", q, kk, vv), ref)
         out, (po, pm, pl) = cw.splitk_partials(q, kk, vv, b, nl, ni, 768, 1)
         fp32_gate(out, ref)
         fp32_gate(po.reshape(out.shape) / pl.reshape(b, nl, 1), ref)
