@@ -337,13 +337,16 @@ void flash16_kernel(Params p) {
     // Q[q0 + 16 cbo + j][32s + 8g .. +7] (96 registers).  K(0) is requested
     // first; no compiler-visible load is pending in the tile loop (where
     // only untracked DMA is in flight).
+    // The Q block arrives by the same DMA as the tiles, row-contiguous 1 KiB
+    // chunks into the buffer of phase 2 (32 latents) or of phases 1 and 2
+    // (64), free until the loop starts, and every wavefront then reads its
+    // operand from LDS.  With 32 latents V(0) is requested at once, behind
+    // K(0) and the Q block; with 64 it waits for the staging buffer.
+    constexpr bool Q_ONE_BUF = BM * LROW <= BUFB;
+    constexpr unsigned QSTAGE = Q_ONE_BUF ? 2 * BUFB : BUFB;
     issue(0);
     {
-        // The Q block arrives by the same DMA as the tiles, row-contiguous
-        // 1 KiB chunks into the buffers of phases 1 and 2 (free until the
-        // loop starts; 64 rows at the tile row stride fill both, 32 one),
-        // and every wavefront then reads its operand from LDS.  Latents past
-        // NL repeat the last one.
+        // Latents past NL repeat the last one.
         constexpr int QCH = BM * (LROW / 16) / kWave;  // 1 KiB chunks of the block
         static_assert(QCH * 1024 == BM * LROW && BM * LROW <= 2 * BUFB, "Q staging");
         const char* qsrc = uniform_ptr((const char*)(p.Q + ((size_t)b * p.NL + q0) * kDim));
@@ -352,18 +355,23 @@ void flash16_kernel(Params p) {
             const int u = kWave * m + lane;
             const int r = min(u / (LROW / 16), qrows - 1);
             const int piece = min(u % (LROW / 16), ROWB / 16 - 1);
-            dma16_untracked(qsrc, (unsigned)(r * ROWB + 16 * piece), lds0 + BUFB + 1024u * m);
+            dma16_untracked(qsrc, (unsigned)(r * ROWB + 16 * piece), lds0 + QSTAGE + 1024u * m);
         }
     }
-    wait_vmcnt<0>();
+    if constexpr (Q_ONE_BUF) {
+        issue(1);
+        wait_vmcnt<CPWV>();  // K(0) and Q landed (wavefront 0: and its first V(0) chunk)
+    } else {
+        wait_vmcnt<0>();
+    }
     lds_barrier();
     v8 qr[KSF];
     {
-        const lds_char* qrd = opaque_lds(lds0 + (unsigned)(BUFB + LROW * (QB * cbo + j) + 16 * g));
+        const lds_char* qrd = opaque_lds(lds0 + (unsigned)(QSTAGE + LROW * (QB * cbo + j) + 16 * g));
 #pragma unroll
         for (int s = 0; s < KSF; ++s) qr[s] = *(const v8*)(qrd + 64 * s);
     }
-    lds_barrier();  // the staging buffers take the tiles of phases 1 and 2 next
+    lds_barrier();  // the staging buffer(s) take the tiles of phases 1 and 2 next
 
     // Per-lane LDS read bases within a tile buffer (fragments differ by
     // immediate offsets): K row 16 kbo + j at byte 16 g (k-step s adds 64 s);
@@ -393,7 +401,7 @@ void flash16_kernel(Params p) {
     XATTN_CLOCK_DECL(pc_wait = 0, pc_qk = 0, pc_pv = 0);
     for (bool first = true;; first = false) {  // passes over the key range; a second is rare
         if (!first) issue(0);
-        issue(1);
+        if (!first || !Q_ONE_BUF) issue(1);
 #pragma unroll
         for (int cl = 0; cl < NCB; ++cl)
 #pragma unroll
