@@ -294,6 +294,42 @@ void flash_f32_kernel(Params p) {
 
     XATTN_STAMP(clk_loop);
     XATTN_CLOCK_DECL(pc_wait = 0, pc_qk = 0, pc_pv = 0);
+    // K and V operand fragments share one ring of three f4, read two 4-MFMA
+    // groups ahead, so the first two fragments of a phase can be read before
+    // it starts.  A QK phase's barrier sits two groups before the end of the
+    // PV phase before it, after the wavefront's last read of that phase's V
+    // buffer: past it, every read of the V buffer is done (the next phase's
+    // DMA refills it) and the next K tile has landed (its DMA was issued a
+    // phase earlier; the chunks issued so far in this phase may still be in
+    // flight), and the first K fragments are read under the last two groups'
+    // MFMAs.  A PV phase's barrier stays after the softmax (the column-split
+    // forms exchange their scores across it; moved into the 64-latent form's
+    // QK phase it measured 0.2-0.5 % slower) and the first V fragments are
+    // read right after it.
+    f4 fr[3];
+    static_assert(NU % 3 == 0, "the fragment ring runs on across phases");
+    constexpr int ISSUED = (NU - 2) / DSTEP + 1 < CPW ? (NU - 2) / DSTEP + 1 : CPW;
+    auto tail_barrier = [&]() {
+        XATTN_STAMP(tw0);
+        wait_vmcnt<ISSUED>();
+        lds_barrier();
+        XATTN_STAMP(tw1);
+        XATTN_CLOCK_ADD(pc_wait, tw0, tw1);
+        XATTN_CLOCK_ADD(pc_pv, tw1, tw0);  // a wait, not PV phase time
+    };
+    // LDS read bases of the K fragments of phase ph (lane (j, g): key j,
+    // columns 16 u + 4 g of this wavefront's part) and the V fragments of
+    // phase ph (group n = NT r + T: V[4 g + r][64 (NT dp + T) + 4 j ..]).
+    auto k_base = [&](int ph) {
+        return lds_base((ph % NBUF) * BUF + j * ROW + 4 * g + 16 * NU * dp);
+    };
+    auto v_base = [&](int ph) {
+        return lds_base((ph % NBUF) * BUF + 4 * j + 4 * g * ROW + 64 * NT * dp);
+    };
+    auto v_frag = [&](lds_cfloat* vb, int n) {
+        return *(lds_cf4*)(vb + (n / NT) * ROW + 64 * (n % NT));
+    };
+
     for (bool first = true;; first = false) {  // passes over the keys; a second is rare
         if (!first) {
             issue(0);
@@ -305,29 +341,31 @@ void flash_f32_kernel(Params p) {
             for (int c = 0; c < 4; ++c) acc[T][c] = (f4){0.f, 0.f, 0.f, 0.f};
         lsum = 0.f;
         over = 0;
+        wait_vmcnt<CPW>();  // phase 0 landed; phase 1 may be in flight
+        lds_barrier();
+        {
+            lds_cfloat* kb = k_base(0);
+            fr[0] = *(lds_cf4*)(kb);
+            fr[1] = *(lds_cf4*)(kb + 16);
+        }
         for (int tile = 0; tile < ntiles; ++tile) {
             const int n0 = k0 + tile * BN;
-            int ph = 2 * tile;
+            const int ph = 2 * tile;
 
             // ---------------- QK phase ----------------
-            XATTN_STAMP(pc_a);
-            wait_vmcnt<CPW>();      // this phase landed; phase ph+1 may be in flight
-            lds_barrier();
             XATTN_STAMP(pc_b);
+            lds_cfloat* const vb = v_base(ph + 1);
             f4 s;
             {
-                // K operand reads run two 4-MFMA groups ahead; the sched_barrier
-                // keeps the scheduler from hoisting all of them.
-                lds_cfloat* kb = lds_base((ph % NBUF) * BUF + j * ROW + 4 * g + 16 * NU * dp);
+                // the sched_barrier keeps the scheduler from hoisting the
+                // fragment reads out of their groups
+                lds_cfloat* kb = k_base(ph);
                 f4 s0 = {0.f, 0.f, 0.f, 0.f}, s1 = s0;
-                f4 kv[3];
-                kv[0] = *(lds_cf4*)(kb);
-                kv[1] = *(lds_cf4*)(kb + 16);
 #pragma unroll
                 for (int u = 0; u < NU; ++u) {
-                    if (u + 2 < NU) kv[(u + 2) % 3] = *(lds_cf4*)(kb + 16 * (u + 2));
+                    if (u + 2 < NU) fr[(u + 2) % 3] = *(lds_cf4*)(kb + 16 * (u + 2));
                     if (u % DSTEP == 0) dma_chunk(ph + 2, u / DSTEP);
-                    const f4 k4 = kv[u % 3];
+                    const f4 k4 = fr[u % 3];
                     s0 = mfma4(k4[0], qr[u][0], s0);
                     s1 = mfma4(k4[1], qr[u][1], s1);
                     s0 = mfma4(k4[2], qr[u][2], s0);
@@ -341,54 +379,54 @@ void flash_f32_kernel(Params p) {
                 softmax(s, n0);
             } else {
                 // this wavefront's share of the block's scores, summed after
-                // the next barrier
+                // the barrier (the previous tile's shares were all read
+                // before the last phase's barrier)
                 *(f4*)(xch + (w * kWave + lane) * 4) = s;
             }
-
-            // ---------------- PV phase ----------------
-            XATTN_STAMP(pc_c);
-            ph += 1;
-            wait_vmcnt<CPW>();
+            XATTN_STAMP(tw0);
+            wait_vmcnt<CPW>();  // the V tile landed; the next K tile may be in flight
             lds_barrier();
-            XATTN_STAMP(pc_d);
+            XATTN_STAMP(tw1);
+            XATTN_CLOCK_ADD(pc_wait, tw0, tw1);
+            fr[0] = v_frag(vb, 0);
+            fr[1] = v_frag(vb, 1);
             if constexpr (DS > 1) {
                 // Every wavefront of the block sums the shares in the same
-                // order, so all of them hold bit-identical scores and weights.
+                // order, so all of them hold bit-identical scores and weights
+                // (the first V fragments are in flight meanwhile).
                 const float* xs = xch + ((w - dp) * kWave + lane) * 4;
                 f4 st = *(const f4*)(xs);
 #pragma unroll
                 for (int d = 1; d < DS; ++d) st += *(const f4*)(xs + d * kWave * 4);
                 softmax(st, n0);
             }
+
+            // ---------------- PV phase ----------------
             {
-                // Group n = NT r + T: V[4g + r][64 (NT dp + T) + 4j .. +3] feeds
-                // the four MFMAs of output tiles (T, c = 0..3) for k-slab r.
-                lds_cfloat* vb = lds_base((ph % NBUF) * BUF + 4 * j + 4 * g * ROW + 64 * NT * dp);
-                f4 vv[3];
-                vv[0] = *(lds_cf4*)(vb);
-                vv[1] = *(lds_cf4*)(vb + (1 / NT) * ROW + 64 * (1 % NT));
+                lds_cfloat* const kn = k_base(ph + 2);  // the next tile's K (read in the tail)
 #pragma unroll
                 for (int n = 0; n < 4 * NT; ++n) {
-                    if (n + 2 < 4 * NT) {
-                        const int rn = (n + 2) / NT, tn = (n + 2) % NT;
-                        vv[(n + 2) % 3] = *(lds_cf4*)(vb + rn * ROW + 64 * tn);
+                    if (n + 2 < 4 * NT) fr[(n + 2) % 3] = v_frag(vb, n + 2);
+                    if (n % DSTEP == 0) dma_chunk(ph + 3, n / DSTEP);
+                    if (n == 4 * NT - 2) {
+                        tail_barrier();
+                        fr[0] = *(lds_cf4*)(kn);
                     }
-                    if (n % DSTEP == 0) dma_chunk(ph + 2, n / DSTEP);
+                    if (n == 4 * NT - 1) fr[1] = *(lds_cf4*)(kn + 16);
                     const int r = n / NT, T = n % NT;
-                    const f4 v4 = vv[n % 3];
+                    const f4 v4 = fr[n % 3];
 #pragma unroll
                     for (int c = 0; c < 4; ++c) acc[T][c] = mfma4(pw[r], v4[c], acc[T][c]);
                     __builtin_amdgcn_sched_barrier(0);
                 }
             }
             XATTN_STAMP(pc_e);
-            XATTN_CLOCK_ADD(pc_wait, pc_a, pc_b);
-            XATTN_CLOCK_ADD(pc_wait, pc_c, pc_d);
-            XATTN_CLOCK_ADD(pc_qk, pc_b, pc_c);
-            XATTN_CLOCK_ADD(pc_pv, pc_d, pc_e);
+            XATTN_CLOCK_ADD(pc_qk, pc_b, tw0);
+            XATTN_CLOCK_ADD(pc_pv, tw1, pc_e);
         }
         // Every wavefront raises the flag (if at all) before this barrier, so
-        // all of them read the same value.
+        // all of them read the same value.  (The last tail read the K buffer
+        // of the phase past the end: data re-read from the range, unused.)
         if (over != 0 && lane == 0) *restart_flag = 1;
         lds_barrier();
         if (!__builtin_amdgcn_readfirstlane(*restart_flag)) break;
