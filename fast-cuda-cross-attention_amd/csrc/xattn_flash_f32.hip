@@ -172,7 +172,6 @@ void flash_f32_kernel(Params p) {
     // the tile loop for zero trips and the split-K instantiation spills.
     __builtin_assume(k1 - k0 >= 1);
     __builtin_assume(ntiles >= 1);
-    const int nphase = 2 * ntiles;
 
     // Phase ph (even: K of tile ph/2, odd: V of tile ph/2) -> buffer ph % 3.
     // Wavefront w's chunks cover tile rows r0 .. r0 + 3, three 1 KiB chunks
@@ -182,11 +181,13 @@ void flash_f32_kernel(Params p) {
     // keys of the tile before; the softmax masks them), and a range shorter
     // than a tile keeps its window at k0 with the rows past the range
     // re-reading its last row (masked too).  Every row read is a key of
-    // [k0, k1), and a chunk's source is one scalar base per phase and row
-    // plus the column offset as the instruction's immediate, with M0 set by
-    // the compiler: every scalar instruction costs issue time here (an fp32
-    // MFMA holds the SIMD while it runs).  The DMA is untracked; the phase
-    // waits below order it.
+    // [k0, k1).  A chunk's source is one scalar base per phase (the window's
+    // first byte), the row's offset in a per-lane register set up once, and
+    // the column as the instruction's immediate; M0 (set by the compiler) is
+    // the buffer's base plus the row's, and the tile loop rotates the three
+    // buffer bases instead of reducing phase numbers modulo 3: every scalar
+    // instruction costs issue time here (an fp32 MFMA holds the SIMD while
+    // it runs).  The DMA is untracked; the phase waits below order it.
     const unsigned lds0 = lds_u32(lds);
     const int r0 = w * (CPW / ROW_CHUNKS);
     const unsigned lane16 = 16u * lane;
@@ -196,23 +197,29 @@ void flash_f32_kernel(Params p) {
     auto win = [&](int n0) {  // n0 = k0 + 16 t
         return nk >= BN ? min(n0, k1 - BN) : n0;
     };
-    int roff[CPW / ROW_CHUNKS];  // byte offsets of this wavefront's rows in a window
+    // lane16 plus the byte offset of each of this wavefront's rows in a window
+    unsigned voff[CPW / ROW_CHUNKS];
 #pragma unroll
-    for (int r = 0; r < CPW / ROW_CHUNKS; ++r) roff[r] = min(r0 + r, min(nk, BN) - 1) * (kDim * 4);
-    auto dma_chunk = [&](int ph, int t) {
-        const int pr = ph < nphase ? ph : ph - 2;
+    for (int r = 0; r < CPW / ROW_CHUNKS; ++r)
+        voff[r] = lane16 + (unsigned)(min(r0 + r, min(nk, BN) - 1) * (kDim * 4));
+    // Chunk t of a phase whose window starts at src (wave-uniform) and whose
+    // LDS buffer starts at byte lds_buf; chunk c of a row adds c KiB to the
+    // row's source and LDS addresses (the instruction's immediate).
+    auto dma_chunk = [&](const char* src, unsigned lds_buf, int t) {
         const int r = t / ROW_CHUNKS, c = t % ROW_CHUNKS;
-        // the row's first LDS byte; chunk c adds c KiB to it and to the source
-        const unsigned row_lds = lds0 + 4u * (unsigned)((ph % NBUF) * BUF + (r0 + r) * ROW);
-        const char* src = (const char*)((pr & 1) ? Vs : Ks) +
-                          ((size_t)win(k0 + (pr >> 1) * BN) * (kDim * 4) + roff[r]);
-        if (c == 0) dma16_m0<0>(src, lane16, row_lds);
-        else if (c == 1) dma16_m0<kWave * 16>(src, lane16, row_lds);
-        else dma16_m0<2 * kWave * 16>(src, lane16, row_lds);
+        const unsigned row_lds = lds_buf + 4u * (unsigned)((r0 + r) * ROW);
+        if (c == 0) dma16_m0<0>(src, voff[r], row_lds);
+        else if (c == 1) dma16_m0<kWave * 16>(src, voff[r], row_lds);
+        else dma16_m0<2 * kWave * 16>(src, voff[r], row_lds);
     };
-    auto issue = [&](int ph) {
+    // the first byte of tile t's window in K or V
+    auto tile_src = [&](const float* base, int t) {
+        return (const char*)base + (size_t)win(k0 + t * BN) * (kDim * 4);
+    };
+    auto issue = [&](int ph) {  // phase 0 or 1 (the first tile's K or V) into buffer ph
+        const char* src = tile_src((ph & 1) ? Vs : Ks, 0);
 #pragma unroll
-        for (int t = 0; t < CPW; ++t) dma_chunk(ph, t);
+        for (int t = 0; t < CPW; ++t) dma_chunk(src, lds0 + 4u * (unsigned)(ph * BUF), t);
     };
 
     // Q^T operand (this wavefront's columns), kept in registers for the whole
@@ -320,11 +327,11 @@ void flash_f32_kernel(Params p) {
     // LDS read bases of the K fragments of phase ph (lane (j, g): key j,
     // columns 16 u + 4 g of this wavefront's part) and the V fragments of
     // phase ph (group n = NT r + T: V[4 g + r][64 (NT dp + T) + 4 j ..]).
-    auto k_base = [&](int ph) {
-        return lds_base((ph % NBUF) * BUF + j * ROW + 4 * g + 16 * NU * dp);
+    auto k_base = [&](int buf) {  // buf: the buffer's first float
+        return lds_base(buf + j * ROW + 4 * g + 16 * NU * dp);
     };
-    auto v_base = [&](int ph) {
-        return lds_base((ph % NBUF) * BUF + 4 * j + 4 * g * ROW + 64 * NT * dp);
+    auto v_base = [&](int buf) {
+        return lds_base(buf + 4 * j + 4 * g * ROW + 64 * NT * dp);
     };
     auto v_frag = [&](lds_cfloat* vb, int n) {
         return *(lds_cf4*)(vb + (n / NT) * ROW + 64 * (n % NT));
@@ -348,23 +355,31 @@ void flash_f32_kernel(Params p) {
             fr[0] = *(lds_cf4*)(kb);
             fr[1] = *(lds_cf4*)(kb + 16);
         }
+        // The buffers of phases 2 tile, 2 tile + 1 and 2 tile + 2 (first
+        // floats), rotated per tile: phase ph reads buffer ph % 3 and refills
+        // buffer (ph + 2) % 3 with the data of phase ph + 2.
+        int bk = 0, bv = BUF, bn = 2 * BUF;
         for (int tile = 0; tile < ntiles; ++tile) {
             const int n0 = k0 + tile * BN;
-            const int ph = 2 * tile;
+            // the next tile's K and V windows (the last tile re-reads its
+            // own: phases past the end, loaded but never read)
+            const int tnext = min(tile + 1, ntiles - 1);
+            const char* const ksrc = tile_src(Ks, tnext);
+            const char* const vsrc = tile_src(Vs, tnext);
 
             // ---------------- QK phase ----------------
             XATTN_STAMP(pc_b);
-            lds_cfloat* const vb = v_base(ph + 1);
+            lds_cfloat* const vb = v_base(bv);
             f4 s;
             {
                 // the sched_barrier keeps the scheduler from hoisting the
                 // fragment reads out of their groups
-                lds_cfloat* kb = k_base(ph);
+                lds_cfloat* kb = k_base(bk);
                 f4 s0 = {0.f, 0.f, 0.f, 0.f}, s1 = s0;
 #pragma unroll
                 for (int u = 0; u < NU; ++u) {
                     if (u + 2 < NU) fr[(u + 2) % 3] = *(lds_cf4*)(kb + 16 * (u + 2));
-                    if (u % DSTEP == 0) dma_chunk(ph + 2, u / DSTEP);
+                    if (u % DSTEP == 0) dma_chunk(ksrc, lds0 + 4u * (unsigned)bn, u / DSTEP);
                     const f4 k4 = fr[u % 3];
                     s0 = mfma4(k4[0], qr[u][0], s0);
                     s1 = mfma4(k4[1], qr[u][1], s1);
@@ -403,11 +418,11 @@ void flash_f32_kernel(Params p) {
 
             // ---------------- PV phase ----------------
             {
-                lds_cfloat* const kn = k_base(ph + 2);  // the next tile's K (read in the tail)
+                lds_cfloat* const kn = k_base(bn);  // the next tile's K (read in the tail)
 #pragma unroll
                 for (int n = 0; n < 4 * NT; ++n) {
                     if (n + 2 < 4 * NT) fr[(n + 2) % 3] = v_frag(vb, n + 2);
-                    if (n % DSTEP == 0) dma_chunk(ph + 3, n / DSTEP);
+                    if (n % DSTEP == 0) dma_chunk(vsrc, lds0 + 4u * (unsigned)bk, n / DSTEP);
                     if (n == 4 * NT - 2) {
                         tail_barrier();
                         fr[0] = *(lds_cf4*)(kn);
@@ -423,6 +438,10 @@ void flash_f32_kernel(Params p) {
             XATTN_STAMP(pc_e);
             XATTN_CLOCK_ADD(pc_qk, pc_b, tw0);
             XATTN_CLOCK_ADD(pc_pv, tw1, pc_e);
+            const int b0 = bk;
+            bk = bn;
+            bn = bv;
+            bv = b0;
         }
         // Every wavefront raises the flag (if at all) before this barrier, so
         // all of them read the same value.  (The last tail read the K buffer
