@@ -593,9 +593,9 @@ void flash16_kernel(Params p) {
             const f4 o = *(const f4*)(stage + r * SROW + 16 * c);
             if (qb + r >= p.NL) continue;
             f4* const at = (f4*)(out_row(qb + r) + d0 + 4 * c);
-            // partials are read back by the merge; the output is not
-            if (PARTIAL) *at = o;
-            else __builtin_nontemporal_store(o, at);
+            // streamed past the caches: the output is not read again, and
+            // the split partials only by the merge, another launch
+            __builtin_nontemporal_store(o, at);
         }
     }
 #ifdef XATTN_PHASE_CLOCK

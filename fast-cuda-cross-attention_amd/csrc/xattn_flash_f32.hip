@@ -485,11 +485,13 @@ void flash_f32_kernel(Params p) {
         for (int T = 0; T < NT; ++T) {
             const f4 o = (f4){acc[T][0][i], acc[T][1][i], acc[T][2][i], acc[T][3][i]} * rsc[i];
             f4* const at = (f4*)(dst + 64 * (NT * dp + T) + 4 * j);
-            // The output is not read again by this launch: streamed past the
-            // caches (measured 1 % faster at 64 latents x 784 keys).  Split
-            // partials stay cached for the merge that reads them next.
-            if (PARTIAL) *at = o;
-            else __builtin_nontemporal_store(o, at);
+            // Streamed past the caches: the output is not read again by this
+            // launch (measured 1 % faster at 64 latents x 784 keys), and the
+            // split partials are read by the merge, another launch whose
+            // workgroups mostly sit on other XCDs, so caching them here only
+            // leaves dirty lines for the end-of-kernel write-back (0.5-2.8 %
+            // faster on split plans, config 1 2.8 %).
+            __builtin_nontemporal_store(o, at);
         }
     }
     if (PARTIAL && dp == 0 && g == 0 && q0 + j < p.NL) {
