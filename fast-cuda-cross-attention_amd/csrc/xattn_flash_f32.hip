@@ -113,6 +113,11 @@ void flash_f32_kernel(Params p) {
     constexpr int NU = 48 / DS;      // 16-column K-operand groups per wavefront
     constexpr int NT = 12 / DS;      // 64-column output tiles per wavefront
     constexpr int DSTEP = NU / CPW;  // MFMA groups per DMA chunk
+    // Score accumulator chains: two in the 64-latent form; one in the
+    // column-split forms, whose scores then stay in VGPRs for the exchange
+    // (no AGPR reads and adds; 0-1.5 % faster there, 0.2 % slower in the
+    // 64-latent form).
+    constexpr int SCH = DS == 1 ? 2 : 1;
     constexpr int XCH = DS > 1 ? NW * kWave * 4 : 0;  // partial-score exchange (floats)
     static_assert(NU % CPW == 0, "DMA spread");
     static_assert((NBUF * BUF + XCH + 4) * 4 <= 160 * 1024, "LDS budget");
@@ -382,12 +387,14 @@ void flash_f32_kernel(Params p) {
                     if (u % DSTEP == 0) dma_chunk(ksrc, lds0 + 4u * (unsigned)bn, u / DSTEP);
                     const f4 k4 = fr[u % 3];
                     s0 = mfma4(k4[0], qr[u][0], s0);
-                    s1 = mfma4(k4[1], qr[u][1], s1);
+                    if constexpr (SCH == 2) s1 = mfma4(k4[1], qr[u][1], s1);
+                    else s0 = mfma4(k4[1], qr[u][1], s0);
                     s0 = mfma4(k4[2], qr[u][2], s0);
-                    s1 = mfma4(k4[3], qr[u][3], s1);
+                    if constexpr (SCH == 2) s1 = mfma4(k4[3], qr[u][3], s1);
+                    else s0 = mfma4(k4[3], qr[u][3], s0);
                     __builtin_amdgcn_sched_barrier(0);
                 }
-                s = s0 + s1;
+                s = SCH == 2 ? s0 + s1 : s0;
             }
 
             if constexpr (DS == 1) {
