@@ -95,6 +95,20 @@ __device__ inline lds_cfloat* opaque_lds_f(const float* lds, int index) {
     return (lds_cfloat*)(uintptr_t)a;
 }
 
+// Maxima of scores as single instructions: fmaxf would first canonicalise
+// each input (v_max_f32 x, x, x) against signalling NaNs, which MFMA results
+// never are; a quiet NaN input is dropped by both alike.
+__device__ inline float vmax(float a, float b) {
+    float r;
+    asm("v_max_f32 %0, %1, %2" : "=v"(r) : "v"(a), "v"(b));
+    return r;
+}
+__device__ inline float vmax3(float a, float b, float c) {
+    float r;
+    asm("v_max3_f32 %0, %1, %2, %3" : "=v"(r) : "v"(a), "v"(b), "v"(c));
+    return r;
+}
+
 __device__ inline f4 mfma4(float a, float b, f4 c) {
     return __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, c, 0, 0, 0);
 }
@@ -253,7 +267,7 @@ void flash_f32_kernel(Params p) {
     // the four lanes of a latent are combined once, at the end of the pass,
     // so the per-tile softmax has no cross-lane step except on the tile
     // that sets the pass's reference.
-    float m_true = -FLT_MAX, m_ref = -FLT_MAX, lsum;
+    float m_true = -FLT_MAX, m_ref = -FLT_MAX, bound = -FLT_MAX, lsum;
     bool ref_set = false;  // the same at every lane of the workgroup
     // Lanes with a score over the pass's bound (a lane mask, so scalar):
     // the pass is checked once, at its end.  Its weights may then have
@@ -280,15 +294,16 @@ void flash_f32_kernel(Params p) {
                 x[i] = (key >= n0 && key < k1) ? s[i] : -INFINITY;
             }
         }
-        const float tmax = fmaxf(fmaxf(x[0], x[1]), fmaxf(x[2], x[3]));
+        const float tmax = vmax(vmax3(x[0], x[1], x[2]), x[3]);
         if (!ref_set) {
             // first tile of the kernel: the reference is the latent's row max
             m_ref = wave_max16_groups(tmax);
+            bound = m_ref + tau_raw;
             ref_set = true;
         }
-        m_true = fmaxf(m_true, tmax);
+        m_true = vmax(m_true, tmax);
         // any lane over the bound <=> the latent's row max over the bound
-        over |= __ballot(tmax > m_ref + tau_raw);
+        over |= __ballot(tmax > bound);
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
             pw[i] = fast_exp2((x[i] - m_ref) * c2);
@@ -463,6 +478,7 @@ void flash_f32_kernel(Params p) {
         lds_barrier();
         if (tid == 0) *restart_flag = 0;
         m_ref = wave_max16_groups(m_true);
+        bound = m_ref + tau_raw;
         lds_barrier();
     }
 
