@@ -29,9 +29,10 @@
 // K and V tiles are shared by the 4 wavefronts through LDS and arrive by
 // global->LDS DMA (16 B per lane, 1 KiB per wave instruction).  Phases
 // alternate QK(t), PV(t); phase p reads buffer p % 3, and the data of phase
-// p + 2 is requested during phase p, one chunk per 16 MFMAs (a burst of 48
-// chunks per CU at the start of a phase stalls every wavefront on the full
-// DMA queue), so every tile has about two phases (~12k cycles) to arrive.
+// p + 2 is requested during phase p, spread over it (one chunk per 16 MFMAs
+// in the 64-latent form: a burst of 48 chunks per CU at the start of a phase
+// stalls every wavefront on the full DMA queue), so every tile has about two
+// phases (~12k cycles in the 64-latent form) to arrive.
 // Phases past the end re-read the last phase of the same kind into the
 // buffer of phase p - 1, whose readers are done, so the loop issues the same
 // way on every tile; the DMA is drained after the loop.  One barrier per
