@@ -12,7 +12,7 @@ import math
 import numpy as np
 import pytest
 
-from conftest import fp32_gate, gate16
+from conftest import TIGHT16, fp32_gate, gate16
 
 pytestmark = pytest.mark.gpu
 
@@ -86,3 +86,42 @@ def test_every_plan_form(cw, oracle, i):
             gate16(out, ref, ref16, precision == "bf16")
         except AssertionError as e:
             raise AssertionError(f"plan {lpw}/{cp}/{s}: {e}") from None
+
+
+@pytest.mark.parametrize("i", range(6))
+def test_scaled_scores_every_plan_form(cw, oracle, i):
+    """Large-magnitude scores (Q scaled by 8 or 16: scaled scores span up to
+    about 70, so 16-bit rows outgrow the first tile's reference by more than
+    the fp16 bound of 2^15 and their passes restart) at seeded ragged shapes,
+    through every workgroup form of both paths under a random split count;
+    16-bit outputs are held to the kernel's own bound against the oracle on
+    the rounded inputs (the unrounded-input contract assumes unit-scale
+    scores)."""
+    rng = np.random.RandomState(4242 + i)
+    b = int(rng.randint(1, 5))
+    nl = int(rng.choice([1, 17, 33, 65, 100]))
+    ni = int(rng.choice([17, 49, 200, 785, 1569]))
+    scale = (8.0, 16.0)[i % 2]
+    q, k, v = oracle.make_inputs(b, nl, ni, 768, seed=9000 + i)
+    q = (q * scale).astype(np.float32)
+    ref = oracle.attention_f64(q, k, v)
+    for lpw in (64, 32, 16):
+        s = int(rng.randint(1, -(-ni // 16) + 1))
+        out, _, _ = cw.benchmark_plan_events(q, k, v, b, nl, ni, 768, lpw, s, warmup=0,
+                                             iters=1)
+        try:
+            fp32_gate(out, ref)
+        except AssertionError as e:
+            raise AssertionError(f"fp32 plan {lpw}/{s}: {e}") from None
+    for precision in ("fp16", "bf16"):
+        bf16 = precision == "bf16"
+        qh, kh, vh = cw._half_inputs(q, k, v, b, 768, bf16)
+        f = oracle.bf16_bits_to_f32 if bf16 else (lambda a: a.astype(np.float32))
+        ref16 = oracle.attention_f64(f(qh).astype(np.float64) * math.sqrt(768), f(kh), f(vh))
+        for lpw, cp in ((64, 1), (64, 2), (32, 1)):
+            s = int(rng.randint(1, -(-ni // 32) + 1))
+            out, _, _ = cw.benchmark_plan_events(q, k, v, b, nl, ni, 768, lpw, s, cp, precision,
+                                                 warmup=0, iters=1)
+            rel = oracle.rel_err(out, ref16)
+            assert np.all(np.isfinite(out)) and rel <= 2 * TIGHT16[bf16], \
+                f"{precision} plan {lpw}/{cp}/{s}: rel vs rounded-input oracle {rel:.3e}"
