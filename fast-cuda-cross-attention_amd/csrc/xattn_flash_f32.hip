@@ -110,6 +110,11 @@ __device__ inline float vmax3(float a, float b, float c) {
     return r;
 }
 
+template <bool B>
+struct Peel {
+    static constexpr bool value = B;
+};
+
 __device__ inline f4 mfma4(float a, float b, f4 c) {
     return __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, c, 0, 0, 0);
 }
@@ -243,9 +248,12 @@ void flash_f32_kernel(Params p) {
     };
 
     // Q^T operand (this wavefront's columns), kept in registers for the whole
-    // key loop.  The wait after the loads leaves no compiler-visible load
-    // pending inside the loop.
+    // key loop, requested behind the first tile's K and V.  The first tile's
+    // QK phase (peeled out of the tile loop) waits for each fragment as it
+    // uses it, so its MFMAs run while the rest of Q arrives, and no
+    // compiler-visible load is pending in the loop itself.
     issue(0);
+    issue(1);
     f4 qr[NU];
     {
         const int qc = min(q0 + j, p.NL - 1);
@@ -253,8 +261,6 @@ void flash_f32_kernel(Params p) {
 #pragma unroll
         for (int u = 0; u < NU; ++u) qr[u] = *(const f4*)(qrow + 16 * u);
     }
-    wait_vmcnt<0>();
-    issue(1);
 
     // The exchange and the flag live in the tile array: a second LDS object
     // would give the LDS reads alias-scope metadata and make the compiler
@@ -358,8 +364,12 @@ void flash_f32_kernel(Params p) {
         return *(lds_cf4*)(vb + (n / NT) * ROW + 64 * (n % NT));
     };
 
-    for (bool first = true;; first = false) {  // passes over the keys; a second is rare
-        if (!first) {
+    // One pass over the keys (a second is rare); FIRST: the first pass,
+    // whose first tile may still be waiting for Q.  Returns whether some
+    // latent's scores outgrew the pass's reference.
+    auto pass = [&](auto first_pass) -> bool {
+        constexpr bool FIRST = decltype(first_pass)::value;
+        if constexpr (!FIRST) {
             issue(0);
             issue(1);
         }
@@ -369,7 +379,8 @@ void flash_f32_kernel(Params p) {
             for (int c = 0; c < 4; ++c) acc[T][c] = (f4){0.f, 0.f, 0.f, 0.f};
         lsum = 0.f;
         over = 0;
-        wait_vmcnt<CPW>();  // phase 0 landed; phase 1 may be in flight
+        if constexpr (FIRST) wait_vmcnt<NU>();  // phases 0 and 1 landed; Q may be in flight
+        else wait_vmcnt<CPW>();                 // phase 0 landed; phase 1 may be in flight
         lds_barrier();
         {
             lds_cfloat* kb = k_base(0);
@@ -380,7 +391,12 @@ void flash_f32_kernel(Params p) {
         // floats), rotated per tile: phase ph reads buffer ph % 3 and refills
         // buffer (ph + 2) % 3 with the data of phase ph + 2.
         int bk = 0, bv = BUF, bn = 2 * BUF;
-        for (int tile = 0; tile < ntiles; ++tile) {
+        // One tile: its QK phase, softmax and PV phase.  PEEL: the first
+        // pass's first tile, whose QK phase may still be waiting for Q (the
+        // compiler waits for each fragment before its MFMAs); it requests
+        // the next tile's K after its MFMAs, so those waits never hold it up.
+        auto tile_body = [&](int tile, auto peel) {
+            constexpr bool PEEL = decltype(peel)::value;
             const int n0 = k0 + tile * BN;
             // the next tile's K and V windows (the last tile re-reads its
             // own: phases past the end, loaded but never read)
@@ -400,7 +416,7 @@ void flash_f32_kernel(Params p) {
 #pragma unroll
                 for (int u = 0; u < NU; ++u) {
                     if (u + 2 < NU) fr[(u + 2) % 3] = *(lds_cf4*)(kb + 16 * (u + 2));
-                    if (u % DSTEP == 0) dma_chunk(ksrc, lds0 + 4u * (unsigned)bn, u / DSTEP);
+                    if (!PEEL && u % DSTEP == 0) dma_chunk(ksrc, lds0 + 4u * (unsigned)bn, u / DSTEP);
                     const f4 k4 = fr[u % 3];
                     s0 = mfma4(k4[0], qr[u][0], s0);
                     if constexpr (SCH == 2) s1 = mfma4(k4[1], qr[u][1], s1);
@@ -411,6 +427,10 @@ void flash_f32_kernel(Params p) {
                     __builtin_amdgcn_sched_barrier(0);
                 }
                 s = SCH == 2 ? s0 + s1 : s0;
+                if constexpr (PEEL) {
+#pragma unroll
+                    for (int t = 0; t < CPW; ++t) dma_chunk(ksrc, lds0 + 4u * (unsigned)bn, t);
+                }
             }
 
             if constexpr (DS == 1) {
@@ -465,22 +485,33 @@ void flash_f32_kernel(Params p) {
             bk = bn;
             bn = bv;
             bv = b0;
-        }
+        };
+        tile_body(0, Peel<FIRST>{});
+        for (int tile = 1; tile < ntiles; ++tile) tile_body(tile, Peel<false>{});
+
         // Every wavefront raises the flag (if at all) before this barrier, so
         // all of them read the same value.  (The last tail read the K buffer
         // of the phase past the end: data re-read from the range, unused.)
         if (over != 0 && lane == 0) *restart_flag = 1;
         lds_barrier();
-        if (!__builtin_amdgcn_readfirstlane(*restart_flag)) break;
-        // Some latent's scores outgrew its reference: drain the DMA (the
-        // re-reads past the last phase may be in flight), clear the flag, and
-        // run the keys again with the reference raised to the max seen so far.
-        wait_vmcnt<0>();
-        lds_barrier();
-        if (tid == 0) *restart_flag = 0;
-        m_ref = wave_max16_groups(m_true);
-        bound = m_ref + tau_raw;
-        lds_barrier();
+        return __builtin_amdgcn_readfirstlane(*restart_flag) != 0;
+    };
+    // The first pass runs outside any loop, so the compiler's waits for the
+    // Q fragments stay in its first tile (inside a loop it would wait for
+    // most of Q before entering it).
+    if (pass(Peel<true>{})) {
+        do {
+            // Some latent's scores outgrew its reference: drain the DMA (the
+            // re-reads past the last phase may be in flight), clear the
+            // flag, and run the keys again with the reference raised to the
+            // max seen so far.
+            wait_vmcnt<0>();
+            lds_barrier();
+            if (tid == 0) *restart_flag = 0;
+            m_ref = wave_max16_groups(m_true);
+            bound = m_ref + tau_raw;
+            lds_barrier();
+        } while (pass(Peel<false>{}));
     }
 
     XATTN_STAMP(clk_loop_end);
