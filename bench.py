@@ -64,6 +64,18 @@ def _time_cpu(fn, seconds):
             return n, el
 
 
+def cpu_model():
+    """The host CPU's model name (Linux /proc/cpuinfo), or None."""
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return None
+
+
 def cpu_baseline(seconds):
     """PyTorch CPU SDPA (the reference's CPU path) on a bounded sample: one
     batch element of the headline workload, repeated for ~``seconds``.  The
@@ -83,6 +95,7 @@ def cpu_baseline(seconds):
         "value": flop / (el / n) / 1e12,
         "unit": "TFLOP/s",
         "cores": torch.get_num_threads(),
+        "cpu_model": cpu_model(),
         "kind": "port",
         "sample": (f"torch CPU scaled_dot_product_attention fp32 on B=1 of the workload "
                    f"(NL={NL} NI={NI} D={D}), {n} calls in {el:.1f} s, "
