@@ -104,6 +104,30 @@ def test_every_plan_form(cw, oracle, bf16, lpw, cp, s):
 
 
 @pytest.mark.parametrize("bf16", [False, True], ids=["fp16", "bf16"])
+@pytest.mark.parametrize("plan", [None, (64, 1, 1), (64, 2, 1), (32, 1, 1), (64, 1, 3)],
+                         ids=["library", "64", "64x2cols", "32", "64split3"])
+def test_closed_forms(cw, oracle, bf16, plan):
+    """Results fixed by the mathematics, not by the oracle:
+    * V = 1 everywhere: every output is sum(round16(p)) / (sum(p) + 1e-6),
+      within one 16-bit rounding of the weights (2^-9 relative in bf16,
+      2^-11 in fp16) of 1;
+    * K = 0: every score is 0, every weight exp2(0) = 1 exactly, so each
+      output row is the mean over the keys of the rounded V the kernel
+      sees, accumulated in fp32 (the reference's 1/(l + 1e-6) included)."""
+    b, nl, ni = 2, 80, 200
+    q, k, v = oracle.make_inputs(b, nl, ni, 768, seed=43)
+    run = (lambda q, k, v: _run(cw, q, k, v, bf16)) if plan is None else \
+        (lambda q, k, v: _run_plan(cw, q, k, v, bf16, *plan))
+    out = run(q, k, np.ones_like(v))
+    assert np.all(np.isfinite(out))
+    assert np.max(np.abs(out - 1.0)) <= (2.0 ** -8 if bf16 else 2.0 ** -10)
+    out = run(q, np.zeros_like(k), v)
+    vr = oracle.round_bf16(v) if bf16 else oracle.round_fp16(v).astype(np.float32)
+    mean = vr.astype(np.float64).sum(axis=1, keepdims=True) / (ni + 1e-6)
+    assert np.max(np.abs(out - mean)) <= 1e-5
+
+
+@pytest.mark.parametrize("bf16", [False, True], ids=["fp16", "bf16"])
 def test_empty_keys(cw, oracle, bf16):
     q, _, _ = oracle.make_inputs(1, 20, 1, 768, seed=1)
     k = np.zeros((1, 0, 768), np.float32)
