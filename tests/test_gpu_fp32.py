@@ -126,6 +126,29 @@ def test_special_cases(cw, oracle):
     assert np.max(np.abs(out - v.mean(axis=1, keepdims=True))) < 1e-5
 
 
+@pytest.mark.parametrize("lpw", [64, 32, 16])
+@pytest.mark.parametrize("s", [1, 3])
+def test_closed_forms_every_plan_form(cw, oracle, lpw, s):
+    """The same closed forms through each fp32 workgroup form, unsplit and
+    split (the merge included): V = 1 gives sum(p) / (sum(p) + 1e-6) = 1 to
+    within 2e-6, and K = 0 gives every weight exp(0) = 1, i.e. the mean of
+    V over the keys, on a ragged shape (a partial last key tile, latents
+    past the last full block)."""
+    b, nl, ni = 2, 70, 150
+    q, k, v = oracle.make_inputs(b, nl, ni, 768, seed=13)
+
+    def run(kk, vv):
+        out, _, _ = cw.benchmark_plan_events(q, kk, vv, b, nl, ni, 768, lpw, s,
+                                             warmup=0, iters=1)
+        return out
+
+    out = run(k, np.ones_like(v))
+    assert np.all(np.isfinite(out)) and np.max(np.abs(out - 1.0)) < 2e-6
+    out = run(np.zeros_like(k), v)
+    mean = v.astype(np.float64).sum(axis=1, keepdims=True) / (ni + 1e-6)
+    assert np.max(np.abs(out - mean)) < 1e-5
+
+
 # ---------------------------------------------------------------------------
 # split-K (launch_splitk_kernel): output and the caller-visible partials
 # ---------------------------------------------------------------------------
